@@ -1,0 +1,264 @@
+/*
+ * MI355X (gfx950) attention / gated-delta-net extension to the rsinfer
+ * plugin ABI v1.
+ *
+ * Everything here is optional for the engine's v1 loader: the loader resolves
+ * only the nine v1 symbols (src/backend/mod.rs:553-575), so the library stays
+ * a drop-in plugin.  A caller that wants the attention and GDN hot path reads
+ * capabilities.flags (plugin-defined, reference header :73) and resolves the
+ * symbols below with dlsym.
+ *
+ * The entry points replace the engine's in-process calls:
+ *   - safetyraise_kernel_kv_*            PagedKvCache (src/engine/state.rs:19-127)
+ *                                        plus SequenceState::checkpoint (:222-224)
+ *   - safetyraise_kernel_attention_forward
+ *                                        the Attention::forward row loop
+ *                                        (src/model/native.rs:615-645): QK-RMSNorm,
+ *                                        RoPE, KV append, causal_attention
+ *                                        (src/model/math.rs:102-155), output gate
+ *   - safetyraise_kernel_gdn_*           RecurrentState (src/engine/state.rs:129-135)
+ *                                        and the Gdn::forward row loop
+ *                                        (src/model/native.rs:720-742):
+ *                                        causal_conv_silu, gated_delta_step,
+ *                                        per-head RMSNorm, silu(z) gate
+ *
+ * Conventions are those of ABI v1: status codes from safetyraise_kernel_status,
+ * text from safetyraise_kernel_last_error, calls on one context are serial.
+ * Every args/options struct starts with struct_size so tail fields can be
+ * added; the plugin rejects a struct_size smaller than the one it knows.
+ *
+ * Pointers are host memory unless SAFETYRAISE_MI355X_DEVICE_POINTERS is set,
+ * in which case every tensor pointer of the call is a device address on the
+ * context's GPU.  Calls return with results complete unless
+ * SAFETYRAISE_MI355X_ASYNC is set (device pointers only): the work is then
+ * enqueued on the context stream, and errors the kernels detect (non-finite
+ * K/V or norm variance, as the reference rejects them) are reported by the
+ * next synchronous call or by safetyraise_kernel_synchronize.
+ */
+#ifndef SAFETYRAISE_MI355X_H
+#define SAFETYRAISE_MI355X_H
+
+#include "safetyraise_kernel.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* capabilities.flags bits reported by this plugin. */
+#define SAFETYRAISE_MI355X_CAP_ATTENTION UINT32_C(0x1)    /* kv_* and attention_forward */
+#define SAFETYRAISE_MI355X_CAP_GDN UINT32_C(0x2)          /* gdn_* */
+#define SAFETYRAISE_MI355X_CAP_DEVICE_STATE UINT32_C(0x4) /* state lives in HBM, O(1) fork */
+
+/* Per-call flags. */
+#define SAFETYRAISE_MI355X_DEVICE_POINTERS UINT32_C(0x1)
+#define SAFETYRAISE_MI355X_ASYNC UINT32_C(0x2)
+#define SAFETYRAISE_MI355X_INPUT_BF16 UINT32_C(0x4)  /* q/k/v (gate, qkv, z, a, b) are bf16 */
+#define SAFETYRAISE_MI355X_QK_NORM UINT32_C(0x8)     /* per-head RMSNorm of q and k */
+#define SAFETYRAISE_MI355X_NORM_OFFSET UINT32_C(0x10) /* weight + 1 (Qwen3.5 norms) */
+#define SAFETYRAISE_MI355X_GATED UINT32_C(0x20)      /* q rows are per-head [q, gate] */
+#define SAFETYRAISE_MI355X_MROPE_INTERLEAVED UINT32_C(0x40)
+
+/* Largest number of sequences one call may carry. */
+#define SAFETYRAISE_MI355X_MAX_BATCH 1024u
+
+/* ------------------------------------------------------------------------
+ * Context helpers (no counterpart in the reference: the v1 calls are
+ * synchronous, these let a device-resident caller order work itself).
+ * ---------------------------------------------------------------------- */
+
+/* Sets the HIP stream (a hipStream_t, NULL = the context's own stream) on
+ * which the context enqueues all later work. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_set_stream(
+    safetyraise_kernel_context *context, void *hip_stream);
+
+/* Waits for the context stream and reports errors detected by kernels of
+ * earlier SAFETYRAISE_MI355X_ASYNC calls (then clears them). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_synchronize(
+    safetyraise_kernel_context *context);
+
+/* ------------------------------------------------------------------------
+ * Paged bf16 KV cache — replaces PagedKvCache (src/engine/state.rs:19-127).
+ *
+ * A pool owns num_pages pages of K and of V in HBM.  One page holds
+ * page_tokens tokens of every KV head, laid out [kv_head][token][head_dim]
+ * in bf16, so one head's page is one contiguous run of
+ * page_tokens*head_dim*2 bytes.  A sequence is a slot holding a page list;
+ * pages are reference counted so kv_fork is O(pages) host work and no device
+ * copy (the snapshot shares every page; the first append into a shared,
+ * partly filled page copies that page, as Arc::make_mut does at state.rs:70).
+ * ---------------------------------------------------------------------- */
+typedef struct safetyraise_kernel_kv_pool safetyraise_kernel_kv_pool;
+
+typedef struct safetyraise_kernel_kv_options {
+    uint32_t struct_size;   /* sizeof(safetyraise_kernel_kv_options) */
+    uint32_t kv_heads;
+    uint32_t head_dim;      /* 64, 128 or 256 */
+    uint32_t page_tokens;   /* tokens per page (reference: 64, state.rs:167) */
+    uint64_t num_pages;     /* pages in the pool */
+    uint64_t max_tokens;    /* per-sequence capacity (max_context) */
+    uint32_t max_sequences; /* sequence slots */
+    uint32_t reserved;
+} safetyraise_kernel_kv_options;
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_create(
+    safetyraise_kernel_context *context, const safetyraise_kernel_kv_options *options,
+    safetyraise_kernel_kv_pool **out_pool);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_destroy(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool);
+
+/* New empty sequence (PagedKvCache::new, state.rs:28-40). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_open(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool,
+    uint32_t *out_sequence);
+/* Snapshot sharing every page (clone for SequenceState::checkpoint). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_fork(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool,
+    uint32_t source, uint32_t *out_sequence);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_close(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool, uint32_t sequence);
+/* PagedKvCache::truncate (state.rs:99-119): len > current length is an error. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_truncate(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool, uint32_t sequence,
+    uint64_t len);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_len(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool, uint32_t sequence,
+    uint64_t *out_len);
+/* Appends tokens rows of already-normalised keys and values, each row
+ * [kv_heads*head_dim] (PagedKvCache::append, state.rs:52-84, repeated).
+ * Values are rounded to bf16 (round to nearest even) unless INPUT_BF16. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_append(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool, uint32_t sequence,
+    const void *keys, const void *values, uint64_t tokens, uint32_t flags);
+/* Reads tokens rows starting at start as f32 [tokens][kv_heads*head_dim],
+ * the layout of PagedKvCache::get (state.rs:86-96).  Host pointers. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_read(
+    safetyraise_kernel_context *context, safetyraise_kernel_kv_pool *pool, uint32_t sequence,
+    uint64_t start, uint64_t tokens, float *keys, float *values);
+
+/* ------------------------------------------------------------------------
+ * Attention — replaces the per-row loop of Attention::forward
+ * (src/model/native.rs:615-645) for a batch of sequences.
+ *
+ * Sequence i contributes seq_rows[i] consecutive rows (its new tokens, in
+ * order).  For each row r at position p:
+ *   q, k  = RMSNorm per head (if QK_NORM; weight+1 if NORM_OFFSET), then RoPE
+ *           (rotate-half over the first rotary_dim dims, angle =
+ *           p / theta^(2i/rotary_dim) in f32, MRoPE axes by mrope_section);
+ *   append (k, v) to the sequence's cache, stored in bf16;
+ *   out   = causal attention of q over every cached token, which is the
+ *           context plus rows 0..r of this call (row r sees len+r+1 keys);
+ *   out  *= sigmoid(gate) if GATED.
+ * Inputs:  q [rows][heads*head_dim] (GATED: [rows][heads][2*head_dim] with the
+ *          gate in the second half of each head), k and v
+ *          [rows][kv_heads*head_dim], f32 or bf16 (INPUT_BF16);
+ *          q_norm, k_norm [head_dim] f32 (QK_NORM only);
+ *          positions [rows][3] int32 (the three MRoPE axes; text uses p,p,p).
+ * Output:  out [rows][heads*head_dim] f32.
+ * seq_ids and seq_rows are always host arrays.  The kernel is chosen per
+ * sequence: up to 16 rows go to the split-K decode/verify kernel, longer
+ * chunks to the MFMA prefill kernel.
+ * ---------------------------------------------------------------------- */
+typedef struct safetyraise_kernel_attention_args {
+    uint32_t struct_size;
+    uint32_t flags;
+    uint32_t heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t rotary_dim;
+    float eps;
+    float rope_theta;
+    uint32_t mrope_section[3]; /* all zero = no MRoPE */
+    uint32_t num_seqs;
+    const uint32_t *seq_ids;
+    const uint32_t *seq_rows;
+    const void *q;
+    const void *k;
+    const void *v;
+    const float *q_norm;
+    const float *k_norm;
+    const int32_t *positions;
+    float *out;
+    safetyraise_kernel_kv_pool *kv;
+} safetyraise_kernel_attention_args;
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
+    safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args);
+
+/* ------------------------------------------------------------------------
+ * Gated delta net — replaces RecurrentState (src/engine/state.rs:129-135)
+ * and the per-row loop of Gdn::forward (src/model/native.rs:720-742).
+ *
+ * A pool holds, per sequence slot, the f32 state [Hv][Dv][Dk] and the
+ * causal-conv history of C = 2*Hk*Dk + Hv*Dv channels.
+ * ---------------------------------------------------------------------- */
+typedef struct safetyraise_kernel_gdn_pool safetyraise_kernel_gdn_pool;
+
+typedef struct safetyraise_kernel_gdn_options {
+    uint32_t struct_size;
+    uint32_t key_heads;
+    uint32_t value_heads;
+    uint32_t key_dim;   /* 128 */
+    uint32_t value_dim; /* 128 */
+    uint32_t conv_kernel;
+    uint32_t max_sequences;
+    uint32_t reserved;
+} safetyraise_kernel_gdn_options;
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_create(
+    safetyraise_kernel_context *context, const safetyraise_kernel_gdn_options *options,
+    safetyraise_kernel_gdn_pool **out_pool);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_destroy(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool);
+/* New sequence with zero state and history (state.rs:167-180). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_open(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool,
+    uint32_t *out_sequence);
+/* Copy of a sequence's state (SequenceState::checkpoint). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_fork(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t source,
+    uint32_t *out_sequence);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_close(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence);
+/* State in the reference layouts: matrix [Hv][Dv][Dk], history [C][K-1]
+ * oldest first.  Host pointers. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_read(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence,
+    float *matrix, float *history);
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_write(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence,
+    const float *matrix, const float *history);
+
+/* For each sequence's rows, in order (src/model/native.rs:720-742):
+ *   x    = silu(causal conv over qkv with the history), history shifted;
+ *   o    = gated_delta_step(x, a, b, A_log, dt_bias) on the state;
+ *   out  = RMSNorm(o per value head, norm, eps, no offset) * silu(z).
+ * Inputs: qkv [rows][C], z [rows][Hv*Dv], a and b [rows][Hv] (f32, or bf16
+ * with INPUT_BF16); a_log, dt_bias [Hv], conv_weight [C][K], norm [Dv] f32.
+ * Output: out [rows][Hv*Dv] f32. */
+typedef struct safetyraise_kernel_gdn_args {
+    uint32_t struct_size;
+    uint32_t flags;
+    float eps;
+    uint32_t num_seqs;
+    const uint32_t *seq_ids;
+    const uint32_t *seq_rows;
+    const void *qkv;
+    const void *z;
+    const void *a;
+    const void *b;
+    const float *a_log;
+    const float *dt_bias;
+    const float *conv_weight;
+    const float *norm;
+    float *out;
+    safetyraise_kernel_gdn_pool *state;
+} safetyraise_kernel_gdn_args;
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
+    safetyraise_kernel_context *context, const safetyraise_kernel_gdn_args *args);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAFETYRAISE_MI355X_H */

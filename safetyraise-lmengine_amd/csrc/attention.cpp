@@ -1,0 +1,243 @@
+// safetyraise_kernel_attention_forward: the Attention::forward row loop of
+// the reference (src/model/native.rs:615-645, projections excluded) for a
+// batch of sequences, on the paged bf16 KV cache of kv.cpp.
+//
+// Argument checks mirror the reference's errors: causal_attention geometry
+// (src/model/math.rs:109-124), apply_rope shape (math.rs:58-65), rms_norm
+// epsilon (math.rs:29-35), KV capacity (src/engine/state.rs:53-55) and empty
+// input (SequenceState::ensure_room, state.rs:208-216).  Non-finite K/V or
+// norm variance are detected on the device; a synchronous call then fails
+// with INVALID_ARGUMENT and the sequences keep their previous length.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "sr_internal.hpp"
+
+namespace sr {
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+struct Region {
+    const void *host;
+    size_t bytes;
+    size_t offset;
+};
+
+uint32_t choose_split(const Ctx *ctx, uint64_t total_tokens, uint32_t kv_heads,
+                      uint32_t page_tokens) {
+    const uint64_t target = 8ull * (uint64_t)ctx->num_cus;
+    uint64_t s = (total_tokens * kv_heads + target - 1) / target;
+    s = (s + 63) / 64 * 64;
+    s = std::max<uint64_t>(s, 64);
+    s = std::min<uint64_t>(s, 4096);
+    const uint64_t page_cap = (uint64_t)(decode_max_split_pages() - 1) * page_tokens / 64 * 64;
+    s = std::min<uint64_t>(s, std::max<uint64_t>(page_cap, 64));
+    return (uint32_t)s;
+}
+
+// One launch of the decode kernel over up to kMetaPerLaunch sequences, each
+// contributing the row `row0` at cache length `ctx`.
+int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
+    MetaPack meta;
+    std::memset(&meta, 0, sizeof meta);
+    uint64_t total_tokens = 0;
+    for (const auto &m : pack) total_tokens += (uint64_t)m.ctx + 1;
+    const uint32_t split = choose_split(ctx, total_tokens, a.kv_heads, a.pool->page_tokens);
+    uint32_t splits = 0;
+    for (size_t i = 0; i < pack.size(); ++i) {
+        meta.m[i] = pack[i];
+        meta.m[i].split0 = splits;
+        splits += (pack[i].ctx + 1 + split - 1) / split;
+    }
+    const uint32_t g = a.heads / a.kv_heads;
+    const size_t rec = (size_t)g * (a.head_dim + 2) * sizeof(float);
+    int32_t st = ensure_buffer(ctx, ctx->partials, (size_t)splits * a.kv_heads * rec, false);
+    if (st != kOk) return st;
+    st = ensure_buffer(ctx, ctx->counters, (size_t)kMetaPerLaunch * a.kv_heads * 4, true);
+    if (st != kOk) return st;
+    SR_HIP(ctx, launch_attn_decode(ctx->stream, a, meta, (int)pack.size(), splits, split,
+                                   (float *)ctx->partials.ptr, (uint32_t *)ctx->counters.ptr));
+    return kOk;
+}
+
+}  // namespace
+
+}  // namespace sr
+
+using namespace sr;
+
+extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
+    safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args) {
+    if (context == nullptr) return kInvalid;
+    Ctx *ctx = context;
+    if (args == nullptr || args->struct_size < sizeof(safetyraise_kernel_attention_args)) {
+        return fail(ctx, kInvalid, "attention args pointer or struct_size is invalid");
+    }
+    const auto &A = *args;
+    auto *pool = A.kv;
+    const uint32_t flags = A.flags;
+    const bool device = (flags & SAFETYRAISE_MI355X_DEVICE_POINTERS) != 0;
+    const bool async = (flags & SAFETYRAISE_MI355X_ASYNC) != 0;
+    const bool bf16 = (flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool gated = (flags & SAFETYRAISE_MI355X_GATED) != 0;
+    const bool qk_norm = (flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
+    if (pool == nullptr) return fail(ctx, kInvalid, "attention needs a KV pool");
+    if (async && !device) return fail(ctx, kInvalid, "ASYNC needs DEVICE_POINTERS");
+    // causal_attention geometry (math.rs:109-124)
+    if (A.heads == 0 || A.kv_heads == 0 || A.head_dim == 0 || A.heads % A.kv_heads != 0 ||
+        A.kv_heads != pool->kv_heads || A.head_dim != pool->head_dim) {
+        return fail(ctx, kInvalid, "attention head mapping or cache geometry is invalid");
+    }
+    if (A.heads / A.kv_heads > 8) {
+        return fail(ctx, kInvalid, "more than 8 query heads per KV head is not supported");
+    }
+    // apply_rope shape (math.rs:58-65)
+    if (A.rotary_dim == 0 || A.rotary_dim > A.head_dim || A.rotary_dim % 2 != 0) {
+        return fail(ctx, kInvalid, "RoPE input shape is invalid");
+    }
+    if (!(A.rope_theta > 0.0f) || !std::isfinite(A.rope_theta)) {
+        return fail(ctx, kInvalid, "RoPE theta must be finite and positive");
+    }
+    if (qk_norm && (!std::isfinite(A.eps) || A.eps <= 0.0f)) {
+        return fail(ctx, kInvalid, "RMSNorm shape or epsilon is invalid");
+    }
+    if (A.num_seqs == 0 || A.num_seqs > SAFETYRAISE_MI355X_MAX_BATCH || A.seq_ids == nullptr ||
+        A.seq_rows == nullptr) {
+        return fail(ctx, kInvalid, "attention batch is empty or too large");
+    }
+    if (A.q == nullptr || A.k == nullptr || A.v == nullptr || A.positions == nullptr ||
+        A.out == nullptr || (qk_norm && (A.q_norm == nullptr || A.k_norm == nullptr))) {
+        return fail(ctx, kInvalid, "attention input or output pointer is NULL");
+    }
+    uint64_t total_rows = 0;
+    uint32_t max_rows = 0;
+    std::vector<uint64_t> row0(A.num_seqs);
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        const uint32_t id = A.seq_ids[i];
+        if (id >= pool->max_sequences || !pool->seqs[id].open) {
+            return fail(ctx, kInvalid, "KV sequence handle is not open");
+        }
+        for (uint32_t j = 0; j < i; ++j) {
+            if (A.seq_ids[j] == id) return fail(ctx, kInvalid, "a sequence appears twice in one call");
+        }
+        if (A.seq_rows[i] == 0) return fail(ctx, kInvalid, "input is empty");  // ensure_room
+        if (pool->seqs[id].len + A.seq_rows[i] > pool->max_tokens) {
+            return fail(ctx, kInvalid, "KV write would exceed the sequence capacity");
+        }
+        row0[i] = total_rows;
+        total_rows += A.seq_rows[i];
+        max_rows = std::max(max_rows, A.seq_rows[i]);
+    }
+    if (total_rows > INT32_MAX) return fail(ctx, kOverflow, "too many rows");
+
+    const size_t esz = bf16 ? 2 : 4;
+    const size_t hs = (size_t)A.head_dim * (gated ? 2 : 1);
+    const size_t q_bytes = total_rows * A.heads * hs * esz;
+    const size_t kv_bytes = total_rows * A.kv_heads * A.head_dim * esz;
+    const size_t pos_bytes = total_rows * 3 * sizeof(int32_t);
+    const size_t norm_bytes = (size_t)A.head_dim * sizeof(float);
+    const size_t out_bytes = total_rows * A.heads * A.head_dim * sizeof(float);
+
+    AttnLaunch L{};
+    L.pool = pool;
+    L.flags = flags;
+    L.heads = A.heads;
+    L.kv_heads = A.kv_heads;
+    L.head_dim = A.head_dim;
+    L.rotary_dim = A.rotary_dim;
+    L.eps = A.eps;
+    std::memcpy(L.mrope, A.mrope_section, sizeof L.mrope);
+    L.err_word = ctx->d_error_word;
+    L.rope = &rope_table(ctx, A.rope_theta, A.rotary_dim);
+    L.q = A.q;
+    L.k = A.k;
+    L.v = A.v;
+    L.q_norm = A.q_norm;
+    L.k_norm = A.k_norm;
+    L.positions = A.positions;
+    L.out = A.out;
+    if (device) {
+        if (((uintptr_t)A.q | (uintptr_t)A.k | (uintptr_t)A.v | (uintptr_t)A.out) & 15u) {
+            return fail(ctx, kInvalid, "device pointers must be 16-byte aligned");
+        }
+    } else {
+        Region regions[6] = {{A.q, q_bytes, 0},         {A.k, kv_bytes, 0},
+                             {A.v, kv_bytes, 0},        {A.positions, pos_bytes, 0},
+                             {A.q_norm, norm_bytes, 0}, {A.k_norm, norm_bytes, 0}};
+        size_t off = 0;
+        for (auto &r : regions) {
+            r.offset = off;
+            off += align_up(r.bytes);
+        }
+        const size_t out_off = off;
+        off += align_up(out_bytes);
+        int32_t st = ensure_buffer(ctx, ctx->staging, off, false);
+        if (st != kOk) return st;
+        char *base = (char *)ctx->staging.ptr;
+        for (auto &r : regions) {
+            if (r.host != nullptr && r.bytes != 0) {
+                SR_HIP(ctx, hipMemcpyAsync(base + r.offset, r.host, r.bytes, hipMemcpyHostToDevice,
+                                           ctx->stream));
+            }
+        }
+        L.q = base + regions[0].offset;
+        L.k = base + regions[1].offset;
+        L.v = base + regions[2].offset;
+        L.positions = (const int32_t *)(base + regions[3].offset);
+        L.q_norm = qk_norm ? (const float *)(base + regions[4].offset) : nullptr;
+        L.k_norm = qk_norm ? (const float *)(base + regions[5].offset) : nullptr;
+        L.out = (float *)(base + out_off);
+    }
+
+    std::vector<uint64_t> old_len(A.num_seqs);
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        old_len[i] = pool->seqs[A.seq_ids[i]].len;
+        int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i]);
+        if (st != kOk) return st;
+    }
+
+    // Row r of every sequence with more than r rows: one decode step each, in
+    // row order, so row r sees the context plus rows 0..r (the reference
+    // appends then attends row by row, native.rs:637-638).
+    for (uint32_t r = 0; r < max_rows; ++r) {
+        std::vector<SeqMeta> pack;
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            if (A.seq_rows[i] <= r) continue;
+            SeqMeta m{};
+            m.slot = A.seq_ids[i];
+            m.ctx = (uint32_t)(old_len[i] + r);
+            m.rows = 1;
+            m.row0 = (uint32_t)(row0[i] + r);
+            pack.push_back(m);
+            if (pack.size() == (size_t)kMetaPerLaunch) {
+                int32_t st = run_decode_pack(ctx, L, pack);
+                if (st != kOk) return st;
+                pack.clear();
+            }
+        }
+        if (!pack.empty()) {
+            int32_t st = run_decode_pack(ctx, L, pack);
+            if (st != kOk) return st;
+        }
+    }
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        pool->seqs[A.seq_ids[i]].len = old_len[i] + A.seq_rows[i];
+    }
+    if (!device) {
+        SR_HIP(ctx, hipMemcpyAsync(A.out, L.out, out_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    int32_t st = finish_call(ctx, async);
+    if (st != kOk && !async) {
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            pool->seqs[A.seq_ids[i]].len = old_len[i];
+        }
+    }
+    return st;
+}

@@ -1,0 +1,103 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "sr_internal.hpp"
+
+namespace sr {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu) != 0u) {
+        return (uint16_t)((u | 0x00400000u) >> 16);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// Reads element i of an f32 or bf16 activation tensor.
+__device__ __forceinline__ float load_act(const void *p, size_t i, bool bf16) {
+    return bf16 ? bf16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
+}
+
+// DPP controls (gfx9 encoding): quad permutes, half-row and row mirrors.
+constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum / max over each aligned group of 16 lanes; every lane of the group ends
+// with the same bits (each step combines a commutative pair).
+__device__ __forceinline__ float sum16(float x) {
+    x += dpp<kDppQuadXor1>(x);
+    x += dpp<kDppQuadXor2>(x);
+    x += dpp<kDppRowHalfMirror>(x);
+    x += dpp<kDppRowMirror>(x);
+    return x;
+}
+__device__ __forceinline__ float max16(float x) {
+    x = fmaxf(x, dpp<kDppQuadXor1>(x));
+    x = fmaxf(x, dpp<kDppQuadXor2>(x));
+    x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppRowMirror>(x));
+    return x;
+}
+// Over the whole 64-lane wave.
+__device__ __forceinline__ float sum64(float x) {
+    x = sum16(x);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+__device__ __forceinline__ float max64(float x) {
+    x = max16(x);
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+
+// MRoPE axis of rotary pair i (src/model/math.rs:69-89).
+__device__ __forceinline__ int rope_axis(uint32_t i, const uint32_t mrope[3], bool interleaved) {
+    if (mrope[0] == 0 && mrope[1] == 0 && mrope[2] == 0) {
+        return 0;
+    }
+    if (interleaved) {
+        if (i % 3 == 1 && i < mrope[1] * 3) return 1;
+        if (i % 3 == 2 && i < mrope[2] * 3) return 2;
+        return 0;
+    }
+    if (i < mrope[0]) return 0;
+    if (i < mrope[0] + mrope[1]) return 1;
+    return 2;
+}
+
+// Reference sigmoid (src/model/math.rs:11-18).
+__device__ __forceinline__ float ref_sigmoid(float x) {
+    if (x >= 0.0f) {
+        return 1.0f / (1.0f + expf(-x));
+    }
+    const float e = expf(x);
+    return e / (1.0f + e);
+}
+
+}  // namespace sr

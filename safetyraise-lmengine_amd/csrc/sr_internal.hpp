@@ -1,0 +1,187 @@
+// Internal declarations shared by the plugin's host code and kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "safetyraise_mi355x.h"
+
+namespace sr {
+
+constexpr int32_t kOk = SAFETYRAISE_KERNEL_STATUS_OK;
+constexpr int32_t kInvalid = SAFETYRAISE_KERNEL_STATUS_INVALID_ARGUMENT;
+constexpr int32_t kUnsupportedDtype = SAFETYRAISE_KERNEL_STATUS_UNSUPPORTED_DTYPE;
+constexpr int32_t kOverflow = SAFETYRAISE_KERNEL_STATUS_DIMENSION_OVERFLOW;
+constexpr int32_t kNoMemory = SAFETYRAISE_KERNEL_STATUS_OUT_OF_MEMORY;
+constexpr int32_t kDeviceError = SAFETYRAISE_KERNEL_STATUS_DEVICE_ERROR;
+constexpr int32_t kInternal = SAFETYRAISE_KERNEL_STATUS_INTERNAL_ERROR;
+constexpr int32_t kAbiMismatch = SAFETYRAISE_KERNEL_STATUS_ABI_MISMATCH;
+
+// Bits of the context's sticky device error word (set by kernels).
+constexpr uint32_t kErrNonFiniteKv = 1u;        // PagedKvCache::append rejects (state.rs:56-58)
+constexpr uint32_t kErrNonFiniteVariance = 2u;  // rms_norm rejects (math.rs:39-41)
+
+// Sequences per kernel launch whose metadata travels in the kernel arguments.
+constexpr int kMetaPerLaunch = 64;
+
+// Grow-only device allocation owned by a context.
+struct DeviceBuffer {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+
+// Per-sequence launch metadata (kernel argument, by value).
+struct SeqMeta {
+    uint32_t slot;    // sequence slot in the pool (page-table row)
+    uint32_t ctx;     // tokens cached before this call's rows
+    uint32_t rows;    // new rows of this sequence in this launch
+    uint32_t row0;    // first row index in the call's q/k/v/out/positions
+    uint32_t split0;  // first global split index (decode kernel)
+};
+
+struct MetaPack {
+    SeqMeta m[kMetaPerLaunch];
+};
+
+// RoPE denominators theta^(2i/rotary_dim) for i < rotary_dim/2, computed on
+// the host with the C library powf in f32 exactly as math.rs:90-91 does.
+struct RopeTable {
+    float denom[128];
+};
+
+}  // namespace sr
+
+struct safetyraise_kernel_context {
+    int device = 0;
+    int num_cus = 256;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string error;
+    uint32_t *d_error_word = nullptr;  // sticky kernel-detected errors
+    sr::DeviceBuffer staging;          // host-pointer mode device copies
+    sr::DeviceBuffer partials;         // split-K partial (m, l, o) records
+    sr::DeviceBuffer counters;         // split-K arrival counters (kept zero between launches)
+    float rope_theta = 0.0f;
+    uint32_t rope_dim = 0;
+    sr::RopeTable rope{};
+};
+
+struct safetyraise_kernel_weight {
+    uint64_t rows = 0;
+    uint64_t cols = 0;
+    uint32_t dtype = 0;
+};
+
+struct safetyraise_kernel_kv_pool {
+    uint32_t kv_heads = 0;
+    uint32_t head_dim = 0;
+    uint32_t page_tokens = 0;
+    uint64_t num_pages = 0;
+    uint64_t max_tokens = 0;
+    uint32_t max_sequences = 0;
+    uint32_t pages_per_seq = 0;  // page-table row length
+    uint16_t *k_pages = nullptr;   // [num_pages][kv_heads][page_tokens][head_dim] bf16
+    uint16_t *v_pages = nullptr;   // same layout
+    int32_t *d_page_table = nullptr;  // [max_sequences][pages_per_seq]
+    struct Sequence {
+        bool open = false;
+        uint64_t len = 0;
+        std::vector<int32_t> pages;
+    };
+    std::vector<Sequence> seqs;
+    std::vector<uint32_t> refcount;
+    std::vector<int32_t> free_pages;
+    size_t page_elems() const { return (size_t)kv_heads * page_tokens * head_dim; }
+};
+
+struct safetyraise_kernel_gdn_pool {
+    uint32_t key_heads = 0;
+    uint32_t value_heads = 0;
+    uint32_t key_dim = 0;
+    uint32_t value_dim = 0;
+    uint32_t conv_kernel = 0;
+    uint32_t max_sequences = 0;
+    uint32_t channels = 0;
+    float *d_state = nullptr;    // [max_sequences][Hv][Dv][Dk]
+    float *d_history = nullptr;  // [max_sequences][C][K-1], oldest first
+    std::vector<uint8_t> open;
+    std::vector<uint32_t> parity;  // which history buffer is current
+    size_t state_elems() const { return (size_t)value_heads * value_dim * key_dim; }
+    size_t history_elems() const { return (size_t)channels * (conv_kernel - 1); }
+};
+
+namespace sr {
+
+using Ctx = safetyraise_kernel_context;
+
+int32_t fail(Ctx *ctx, int32_t status, const std::string &message);
+int32_t hip_fail(Ctx *ctx, hipError_t err, const char *what);
+#define SR_HIP(ctx, expr)                                    \
+    do {                                                     \
+        hipError_t _e = (expr);                              \
+        if (_e != hipSuccess) return ::sr::hip_fail((ctx), _e, #expr); \
+    } while (0)
+
+bool checked_mul(uint64_t a, uint64_t b, uint64_t *out);
+int32_t ensure_buffer(Ctx *ctx, DeviceBuffer &buf, size_t bytes, bool zero);
+int32_t finish_call(Ctx *ctx, bool async);  // sync + sticky error check unless async
+const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim);
+
+// KV pool helpers used by attention.
+int32_t kv_prepare_append(Ctx *ctx, safetyraise_kernel_kv_pool *pool, uint32_t seq, uint64_t n);
+
+// ---------------- kernel launchers (defined in the .hip files) ----------------
+hipError_t launch_page_table_set(hipStream_t s, int32_t *table, const uint32_t *idx,
+                                 const int32_t *val, int n);
+hipError_t launch_kv_scatter(hipStream_t s, const safetyraise_kernel_kv_pool *pool, uint32_t slot,
+                             uint64_t start, uint64_t tokens, const void *keys, const void *values,
+                             bool bf16_in, uint32_t *err_word);
+hipError_t launch_kv_gather(hipStream_t s, const safetyraise_kernel_kv_pool *pool, uint32_t slot,
+                            uint64_t start, uint64_t tokens, float *keys, float *values);
+hipError_t launch_page_copy(hipStream_t s, const safetyraise_kernel_kv_pool *pool, int32_t dst,
+                            int32_t src);
+
+struct AttnLaunch {
+    const safetyraise_kernel_kv_pool *pool;
+    uint32_t flags;
+    uint32_t heads, kv_heads, head_dim, rotary_dim;
+    float eps;
+    uint32_t mrope[3];
+    const void *q, *k, *v;
+    const float *q_norm, *k_norm;
+    const int32_t *positions;
+    float *out;
+    uint32_t *err_word;
+    const RopeTable *rope;
+};
+
+// Decode: every sequence of the pack has rows == 1.  splits_total and
+// split_tokens describe the split-K grid; partials/counters are scratch.
+hipError_t launch_attn_decode(hipStream_t s, const AttnLaunch &a, const MetaPack &meta, int nseq,
+                              uint32_t splits_total, uint32_t split_tokens, float *partials,
+                              uint32_t *counters);
+uint32_t decode_max_split_pages();
+
+struct GdnLaunch {
+    const safetyraise_kernel_gdn_pool *pool;
+    const void *qkv, *z, *a, *b;
+    const float *a_log, *dt_bias, *conv_w, *norm;
+    float *raw, *out;
+    uint32_t *err_word;
+    float eps;
+    bool bf16_in;
+};
+
+// Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
+hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,
+                      const uint32_t *rows, const uint32_t *row0, const uint32_t *parity, int nseq,
+                      uint32_t total_rows);
+uint32_t gdn_key_dim();
+uint32_t gdn_row_block();
+uint32_t gdn_max_kernel();
+
+}  // namespace sr
