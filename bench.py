@@ -42,7 +42,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode"])
+    p.add_argument("--workload", default="decode", choices=["decode", "copy"])
     p.add_argument("--layers", type=int, default=36)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=0x5A5A0001)
@@ -70,7 +70,8 @@ def bench_decode(args, torch, pkg):
     pages = int(sum((L + total_steps + page) // page + 1 for L in lengths)) + 8
 
     backend = pkg.NativeBackend.load()
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()  # default priority
+    torch.cuda.set_stream(stream)
     backend.set_stream(stream.cuda_stream)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(args.seed)
@@ -248,6 +249,28 @@ def cpu_baseline_decode(pkg, pool, seqs, lens, q, k, v, pos, gq, gk, heads, kvh,
     }
 
 
+def bench_copy(args, torch):
+    """Calibration: a plain device copy of a known size (for PMC byte counters)."""
+    nbytes = 1 << 30
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        b.copy_(a)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    return {"metric": "device copy GB/s (calibration)", "value": round(2 * nbytes / ms / 1e6, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "copy 1 GiB read + 1 GiB write"}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -262,6 +285,8 @@ def main():
     pkg = importlib.import_module("safetyraise-lmengine_amd")
     if args.workload == "decode":
         result = bench_decode(args, torch, pkg)
+    else:
+        result = bench_copy(args, torch)
     print(json.dumps(result), flush=True)
 
 

@@ -80,9 +80,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_synchronize(
  * Paged bf16 KV cache — replaces PagedKvCache (src/engine/state.rs:19-127).
  *
  * A pool owns num_pages pages of K and of V in HBM.  One page holds
- * page_tokens tokens of every KV head, laid out [kv_head][token][head_dim]
- * in bf16, so one head's page is one contiguous run of
- * page_tokens*head_dim*2 bytes.  A sequence is a slot holding a page list;
+ * page_tokens tokens of every KV head in bf16; the pool is head-major,
+ * [kv_head][page][token][head_dim], so a sequence whose pages are adjacent
+ * is one contiguous stream per head.  A sequence is a slot holding a page list;
  * pages are reference counted so kv_fork is O(pages) host work and no device
  * copy (the snapshot shares every page; the first append into a shared,
  * partly filled page copies that page, as Arc::make_mut does at state.rs:70).
@@ -93,7 +93,7 @@ typedef struct safetyraise_kernel_kv_options {
     uint32_t struct_size;   /* sizeof(safetyraise_kernel_kv_options) */
     uint32_t kv_heads;
     uint32_t head_dim;      /* 64, 128 or 256 */
-    uint32_t page_tokens;   /* tokens per page (reference: 64, state.rs:167) */
+    uint32_t page_tokens;   /* power of two >= 16 (reference: 64, state.rs:167) */
     uint64_t num_pages;     /* pages in the pool */
     uint64_t max_tokens;    /* per-sequence capacity (max_context) */
     uint32_t max_sequences; /* sequence slots */

@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -30,40 +31,25 @@ struct Region {
     size_t offset;
 };
 
-uint32_t choose_split(const Ctx *ctx, uint64_t total_tokens, uint32_t kv_heads,
-                      uint32_t page_tokens) {
-    const uint64_t target = 8ull * (uint64_t)ctx->num_cus;
-    uint64_t s = (total_tokens * kv_heads + target - 1) / target;
-    s = (s + 63) / 64 * 64;
-    s = std::max<uint64_t>(s, 64);
-    s = std::min<uint64_t>(s, 4096);
-    const uint64_t page_cap = (uint64_t)(decode_max_split_pages() - 1) * page_tokens / 64 * 64;
-    s = std::min<uint64_t>(s, std::max<uint64_t>(page_cap, 64));
-    return (uint32_t)s;
+float *reserve_partials(void *user, size_t bytes) {
+    Ctx *ctx = (Ctx *)user;
+    if (ensure_buffer(ctx, ctx->partials, bytes, false) != kOk) {
+        return nullptr;
+    }
+    return (float *)ctx->partials.ptr;
 }
 
-// One launch of the decode kernel over up to kMetaPerLaunch sequences, each
+// One launch of the decode kernels over up to kMetaPerLaunch sequences, each
 // contributing the row `row0` at cache length `ctx`.
 int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
-    MetaPack meta;
-    std::memset(&meta, 0, sizeof meta);
-    uint64_t total_tokens = 0;
-    for (const auto &m : pack) total_tokens += (uint64_t)m.ctx + 1;
-    const uint32_t split = choose_split(ctx, total_tokens, a.kv_heads, a.pool->page_tokens);
-    uint32_t splits = 0;
-    for (size_t i = 0; i < pack.size(); ++i) {
-        meta.m[i] = pack[i];
-        meta.m[i].split0 = splits;
-        splits += (pack[i].ctx + 1 + split - 1) / split;
+    DecodePlanInput plan{ctx->num_cus, reserve_partials, ctx};
+    const hipError_t e = launch_attn_decode(ctx->stream, a, pack.data(), (int)pack.size(), plan);
+    if (e != hipSuccess) {
+        if (ctx->error.empty() || e != hipErrorOutOfMemory) {
+            return hip_fail(ctx, e, "decode attention launch");
+        }
+        return kNoMemory;  // ensure_buffer already set the text
     }
-    const uint32_t g = a.heads / a.kv_heads;
-    const size_t rec = (size_t)g * (a.head_dim + 2) * sizeof(float);
-    int32_t st = ensure_buffer(ctx, ctx->partials, (size_t)splits * a.kv_heads * rec, false);
-    if (st != kOk) return st;
-    st = ensure_buffer(ctx, ctx->counters, (size_t)kMetaPerLaunch * a.kv_heads * 4, true);
-    if (st != kOk) return st;
-    SR_HIP(ctx, launch_attn_decode(ctx->stream, a, meta, (int)pack.size(), splits, split,
-                                   (float *)ctx->partials.ptr, (uint32_t *)ctx->counters.ptr));
     return kOk;
 }
 
@@ -208,6 +194,7 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     // appends then attends row by row, native.rs:637-638).
     for (uint32_t r = 0; r < max_rows; ++r) {
         std::vector<SeqMeta> pack;
+        uint64_t pack_tokens = 0;
         for (uint32_t i = 0; i < A.num_seqs; ++i) {
             if (A.seq_rows[i] <= r) continue;
             SeqMeta m{};
@@ -215,11 +202,19 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
             m.ctx = (uint32_t)(old_len[i] + r);
             m.rows = 1;
             m.row0 = (uint32_t)(row0[i] + r);
+            if (!pack.empty() && pack_tokens + m.ctx + 1 > 0x7fffffffull) {
+                int32_t st = run_decode_pack(ctx, L, pack);
+                if (st != kOk) return st;
+                pack.clear();
+                pack_tokens = 0;
+            }
             pack.push_back(m);
+            pack_tokens += (uint64_t)m.ctx + 1;
             if (pack.size() == (size_t)kMetaPerLaunch) {
                 int32_t st = run_decode_pack(ctx, L, pack);
                 if (st != kOk) return st;
                 pack.clear();
+                pack_tokens = 0;
             }
         }
         if (!pack.empty()) {

@@ -1,10 +1,10 @@
 // Paged KV cache data movement: page-table updates, raw row append (scatter)
 // and row read-back (gather) in the reference's token-major row layout.
 //
-// Page layout in HBM: [page][kv_head][page_tokens][head_dim] bf16, so one
-// head's share of a page is contiguous.  A reference row (one token,
+// Pool layout in HBM: [kv_head][page][page_tokens][head_dim] bf16 (head
+// major), so a head's pages are adjacent.  A reference row (one token,
 // [kv_head][head_dim], src/engine/state.rs:90-95) is spread over kv_heads
-// runs of head_dim values.
+// runs of head_dim values, one per head region.
 #include "sr_device.hpp"
 
 namespace sr {
@@ -36,6 +36,7 @@ struct ScatterParams {
     uint32_t *err_word;
     uint64_t start;
     uint64_t tokens;
+    uint64_t num_pages;
     uint32_t kv_heads;
     uint32_t head_dim;
     uint32_t page_tokens;
@@ -54,7 +55,7 @@ __global__ void kv_scatter_kernel(const ScatterParams p) {
         const uint64_t t = th / p.kv_heads;
         const uint64_t tok = p.start + t;
         const int32_t page = p.table[tok / p.page_tokens];
-        const size_t dst = (((size_t)page * p.kv_heads + h) * p.page_tokens + tok % p.page_tokens) *
+        const size_t dst = (((size_t)h * p.num_pages + page) * p.page_tokens + tok % p.page_tokens) *
                                p.head_dim + (size_t)c * 8;
         const size_t src = (t * p.kv_heads + h) * (size_t)p.head_dim + (size_t)c * 8;
         uint4 kw, vw;
@@ -100,6 +101,7 @@ struct GatherParams {
     float *values;
     uint64_t start;
     uint64_t tokens;
+    uint64_t num_pages;
     uint32_t kv_heads;
     uint32_t head_dim;
     uint32_t page_tokens;
@@ -117,7 +119,7 @@ __global__ void kv_gather_kernel(const GatherParams p) {
         const uint64_t tok = p.start + t;
         const int32_t page = p.table[tok / p.page_tokens];
         const size_t src =
-            (((size_t)page * p.kv_heads + h) * p.page_tokens + tok % p.page_tokens) * p.head_dim + d;
+            (((size_t)h * p.num_pages + page) * p.page_tokens + tok % p.page_tokens) * p.head_dim + d;
         p.keys[i] = bf16_to_f32(p.k_pages[src]);
         p.values[i] = bf16_to_f32(p.v_pages[src]);
     }
@@ -160,6 +162,7 @@ hipError_t launch_kv_scatter(hipStream_t s, const safetyraise_kernel_kv_pool *po
     p.err_word = err_word;
     p.start = start;
     p.tokens = tokens;
+    p.num_pages = pool->num_pages;
     p.kv_heads = pool->kv_heads;
     p.head_dim = pool->head_dim;
     p.page_tokens = pool->page_tokens;
@@ -180,6 +183,7 @@ hipError_t launch_kv_gather(hipStream_t s, const safetyraise_kernel_kv_pool *poo
     p.values = values;
     p.start = start;
     p.tokens = tokens;
+    p.num_pages = pool->num_pages;
     p.kv_heads = pool->kv_heads;
     p.head_dim = pool->head_dim;
     p.page_tokens = pool->page_tokens;
@@ -190,14 +194,16 @@ hipError_t launch_kv_gather(hipStream_t s, const safetyraise_kernel_kv_pool *poo
 
 hipError_t launch_page_copy(hipStream_t s, const safetyraise_kernel_kv_pool *pool, int32_t dst,
                             int32_t src) {
-    const size_t bytes = pool->page_elems() * sizeof(uint16_t);
-    hipError_t e = hipMemcpyAsync(pool->k_pages + (size_t)dst * pool->page_elems(),
-                                  pool->k_pages + (size_t)src * pool->page_elems(), bytes,
-                                  hipMemcpyDeviceToDevice, s);
+    // one PT x D block per head, the heads head_stride() elements apart
+    const size_t width = pool->head_page_elems() * sizeof(uint16_t);
+    const size_t pitch = pool->head_stride() * sizeof(uint16_t);
+    const size_t d_off = (size_t)dst * pool->head_page_elems();
+    const size_t s_off = (size_t)src * pool->head_page_elems();
+    hipError_t e = hipMemcpy2DAsync(pool->k_pages + d_off, pitch, pool->k_pages + s_off, pitch,
+                                    width, pool->kv_heads, hipMemcpyDeviceToDevice, s);
     if (e != hipSuccess) return e;
-    return hipMemcpyAsync(pool->v_pages + (size_t)dst * pool->page_elems(),
-                          pool->v_pages + (size_t)src * pool->page_elems(), bytes,
-                          hipMemcpyDeviceToDevice, s);
+    return hipMemcpy2DAsync(pool->v_pages + d_off, pitch, pool->v_pages + s_off, pitch, width,
+                            pool->kv_heads, hipMemcpyDeviceToDevice, s);
 }
 
 }  // namespace sr

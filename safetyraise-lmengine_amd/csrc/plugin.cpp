@@ -128,7 +128,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_create_context(
             prop.multiProcessorCount > 0) {
             ctx->num_cus = prop.multiProcessorCount;
         }
-        err = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+        // A blocking stream: ordered with the legacy default stream, so work a
+        // caller queues there (e.g. a framework's allocations) precedes ours.
+        err = hipStreamCreate(&ctx->own_stream);
     }
     if (err == hipSuccess) {
         ctx->stream = ctx->own_stream;
@@ -156,7 +158,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_context(
     if (hipStreamSynchronize(context->stream) != hipSuccess) {
         status = kDeviceError;
     }
-    for (DeviceBuffer *b : {&context->staging, &context->partials, &context->counters}) {
+    for (DeviceBuffer *b : {&context->staging, &context->partials}) {
         if (b->ptr != nullptr) (void)hipFree(b->ptr);
     }
     if (context->d_error_word != nullptr) (void)hipFree(context->d_error_word);

@@ -30,6 +30,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
+// acc + a.lo*b.lo + a.hi*b.hi for packed bf16 pairs, f32 accumulation
+// (the products of two bf16 values are exact in f32).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
 // Reads element i of an f32 or bf16 activation tensor.
 __device__ __forceinline__ float load_act(const void *p, size_t i, bool bf16) {
     return bf16 ? bf16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];

@@ -64,7 +64,6 @@ struct safetyraise_kernel_context {
     uint32_t *d_error_word = nullptr;  // sticky kernel-detected errors
     sr::DeviceBuffer staging;          // host-pointer mode device copies
     sr::DeviceBuffer partials;         // split-K partial (m, l, o) records
-    sr::DeviceBuffer counters;         // split-K arrival counters (kept zero between launches)
     float rope_theta = 0.0f;
     uint32_t rope_dim = 0;
     sr::RopeTable rope{};
@@ -84,8 +83,11 @@ struct safetyraise_kernel_kv_pool {
     uint64_t max_tokens = 0;
     uint32_t max_sequences = 0;
     uint32_t pages_per_seq = 0;  // page-table row length
-    uint16_t *k_pages = nullptr;   // [num_pages][kv_heads][page_tokens][head_dim] bf16
-    uint16_t *v_pages = nullptr;   // same layout
+    // Head-major pool: [kv_heads][num_pages][page_tokens][head_dim] bf16, so
+    // one head's pages are adjacent and a sequence on consecutive pages is
+    // one contiguous stream per head.
+    uint16_t *k_pages = nullptr;
+    uint16_t *v_pages = nullptr;
     int32_t *d_page_table = nullptr;  // [max_sequences][pages_per_seq]
     struct Sequence {
         bool open = false;
@@ -96,6 +98,8 @@ struct safetyraise_kernel_kv_pool {
     std::vector<uint32_t> refcount;
     std::vector<int32_t> free_pages;
     size_t page_elems() const { return (size_t)kv_heads * page_tokens * head_dim; }
+    size_t head_page_elems() const { return (size_t)page_tokens * head_dim; }
+    size_t head_stride() const { return (size_t)num_pages * page_tokens * head_dim; }
 };
 
 struct safetyraise_kernel_gdn_pool {
@@ -159,12 +163,21 @@ struct AttnLaunch {
     const RopeTable *rope;
 };
 
-// Decode: every sequence of the pack has rows == 1.  splits_total and
-// split_tokens describe the split-K grid; partials/counters are scratch.
-hipError_t launch_attn_decode(hipStream_t s, const AttnLaunch &a, const MetaPack &meta, int nseq,
-                              uint32_t splits_total, uint32_t split_tokens, float *partials,
-                              uint32_t *counters);
-uint32_t decode_max_split_pages();
+// Host inputs of the decode launch plan: the CU count and a way to get the
+// scratch for per-segment (max, sum, output) records (context-owned, grown
+// on demand; returns nullptr when it cannot be allocated).
+struct DecodePlanInput {
+    int num_cus;
+    float *(*reserve)(void *user, size_t bytes);
+    void *user;
+    float *reserve_partials(size_t bytes) const { return reserve(user, bytes); }
+};
+
+// Decode: one new row per sequence (seqs[i].ctx tokens cached before it,
+// row seqs[i].row0 of the call's tensors).  Up to kMetaPerLaunch sequences
+// whose visible tokens sum below 2^31.
+hipError_t launch_attn_decode(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
+                              const DecodePlanInput &in);
 
 struct GdnLaunch {
     const safetyraise_kernel_gdn_pool *pool;

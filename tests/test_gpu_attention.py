@@ -125,7 +125,7 @@ def new_pool(pkg, backend, kv_heads, dim, page_tokens=64, max_tokens=4096, seqs=
 def test_kv_append_read_layout(pkg, backend):
     # src/gpu.rs:6467-6488: token rows [kv_head][dim] read back unchanged; the
     # reference vector's head_dim 2 sits in the first two dims of each head.
-    pool = new_pool(pkg, backend, 2, 64, page_tokens=4, max_tokens=8, seqs=2)
+    pool = new_pool(pkg, backend, 2, 64, page_tokens=16, max_tokens=8, seqs=2)
     seq = pool.open()
     rows_k = np.zeros((2, 128), np.float32)
     rows_v = np.zeros((2, 128), np.float32)
@@ -147,7 +147,7 @@ def test_kv_append_read_layout(pkg, backend):
 
 def test_kv_truncate_restores_without_losing_prior_rows(pkg, backend):
     # src/gpu.rs:6490-6518
-    pool = new_pool(pkg, backend, 1, 64, page_tokens=4, max_tokens=8, seqs=2)
+    pool = new_pool(pkg, backend, 1, 64, page_tokens=16, max_tokens=8, seqs=2)
     seq = pool.open()
     row = lambda a, b: np.array([[a, b] + [0.0] * 62], np.float32)
     pool.append(seq, row(1, 2), row(3, 4))
@@ -163,37 +163,48 @@ def test_kv_truncate_restores_without_losing_prior_rows(pkg, backend):
     pool.destroy()
 
 
-def test_kv_snapshot_isolated_across_partial_and_full_pages(pkg, backend):
-    # src/engine/state.rs tests: width 2 (here dims 0..1 of one 64-wide head),
-    # 9 tokens max, 4-token pages; fork = checkpoint()
-    pool = new_pool(pkg, backend, 1, 64, page_tokens=4, max_tokens=9, seqs=4)
+@pytest.mark.parametrize("scale", [1, 4])
+def test_kv_snapshot_isolated_across_partial_and_full_pages(pkg, backend, scale):
+    # src/engine/state.rs tests: width 2 (dims 0..1 of one 64-wide head), 9
+    # tokens max, fork = checkpoint().  The reference pages hold 4 tokens; the
+    # pool's smallest page is 16, so scale 4 multiplies every token count by 4
+    # to keep the same full-page / partial-page pattern (scale 1 keeps the
+    # reference's counts, all inside one page).
+    n_max, n_fork, n_trunc = 9 * scale, 3 * scale, 2 * scale
+    pool = new_pool(pkg, backend, 1, 64, page_tokens=16, max_tokens=n_max, seqs=4)
     seq = pool.open()
     row = lambda a, b: np.array([[a, b] + [0.0] * 62], np.float32)
-    for n in range(3):
+    for n in range(n_fork):
         pool.append(seq, row(n, 1.0), row(2.0, n))
     saved = pool.fork(seq)
-    for n in range(3, 9):
+    for n in range(n_fork, n_max):
         pool.append(seq, row(n, 1.0), row(2.0, n))
     with pytest.raises(pkg.PluginError):
         pool.append(seq, row(1, 1), row(1, 1))
-    pool.truncate(seq, 2)
+    pool.truncate(seq, n_trunc)
     pool.append(seq, row(99, 99), row(88, 88))
-    assert list(pool.read(saved, 2, 1)[0][0, :2]) == [2.0, 1.0]
-    assert list(pool.read(seq, 2, 1)[0][0, :2]) == [99.0, 99.0]
+    assert list(pool.read(saved, n_trunc, 1)[0][0, :2]) == [float(n_trunc), 1.0]
+    assert list(pool.read(seq, n_trunc, 1)[0][0, :2]) == [99.0, 99.0]
     with pytest.raises(pkg.PluginError):
-        pool.read(saved, 3, 1)
+        pool.read(saved, n_fork, 1)
     with pytest.raises(pkg.PluginError):
-        pool.truncate(seq, 4)
+        pool.truncate(seq, n_trunc + 2)
     pool.truncate(seq, 0)
     assert pool.len(seq) == 0
-    # the snapshot still reads its own three rows after the original moved on
+    # the snapshot still reads its own rows after the original moved on
     k, _ = pool.read(saved)
-    assert list(k[:, 0]) == [0.0, 1.0, 2.0]
+    assert list(k[:, 0]) == [float(n) for n in range(n_fork)]
     pool.destroy()
 
 
+def test_kv_pool_rejects_unsupported_page_sizes(pkg, backend):
+    for pt in (4, 24, 100):
+        with pytest.raises(pkg.PluginError):
+            pkg.KvCache(backend, 1, 64, pt, 8, 64, 1)
+
+
 def test_kv_append_rejects_non_finite_and_keeps_length(pkg, backend):
-    pool = new_pool(pkg, backend, 1, 64, page_tokens=4, max_tokens=8, seqs=1)
+    pool = new_pool(pkg, backend, 1, 64, page_tokens=16, max_tokens=8, seqs=1)
     seq = pool.open()
     good = np.ones((1, 64), np.float32)
     pool.append(seq, good, good)
@@ -253,11 +264,12 @@ def test_qwen35_gated_partial_rope_mrope(pkg, backend, rng):
     pool.destroy()
 
 
-@pytest.mark.parametrize("ctx,rows", [(300, 5), (1000, 37), (0, 9)])
-def test_multi_row_call_is_causal_row_by_row(pkg, backend, rng, ctx, rows):
+@pytest.mark.parametrize("ctx,rows,page", [(300, 5, 64), (1000, 37, 64), (0, 9, 64),
+                                           (300, 5, 16), (1000, 37, 32)])
+def test_multi_row_call_is_causal_row_by_row(pkg, backend, rng, ctx, rows, page):
     # row r sees the context plus rows 0..r (native.rs:637-638); ctx 0 is a
     # fresh prompt
-    pool = new_pool(pkg, backend, 8, 128, max_tokens=2048, seqs=2)
+    pool = new_pool(pkg, backend, 8, 128, page_tokens=page, max_tokens=2048, seqs=2)
     gq = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
     gk = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
     cases = [Case(rng, pool, 32, 8, 128, ctx=ctx, rows=rows),
