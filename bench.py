@@ -195,7 +195,9 @@ def bench_decode(args, torch, pkg):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("attn_decode_qwen3_8b"),
-            "kernel": "attn_decode_kernel<128,4>",
+            # one decode call = the split-K kernel plus its small combine pass;
+            # the events bracket both (rocprofv3 lists them separately)
+            "kernel": "attn_decode_kernel<128,4> + attn_combine_kernel<128,4>",
             "launch_us_mean": round(float(launch_us.mean()), 2),
             "bytes_per_launch": int(per_launch_bytes),
         },
