@@ -42,7 +42,10 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "copy"])
+    p.add_argument("--workload", default="decode", choices=["decode", "prefill", "copy"])
+    p.add_argument("--no-prefill", action="store_true",
+                   help="decode workload only (skip the prefill figure of the same line)")
+    p.add_argument("--prefill-steps", type=int, default=5)
     p.add_argument("--layers", type=int, default=36)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=0x5A5A0001)
@@ -251,6 +254,163 @@ def cpu_baseline_decode(pkg, pool, seqs, lens, q, k, v, pos, gq, gk, heads, kvh,
     }
 
 
+def bench_prefill(args, torch, pkg, steps, warmup):
+    """Qwen3-8B chunked causal prefill attention.
+
+    4 sequences x 4096 tokens appended in chunks of 512 (8 calls of 4 x 512
+    rows), 32 Q / 8 KV heads, head_dim 128, QK-RMSNorm + RoPE theta 1e6, bf16
+    inputs ~N(0,1), bf16 KV.  One step is the whole 4096-token prefill of one
+    layer (the cache is truncated to empty before each step).  FLOPs count the
+    causal work exactly: 4 * head_dim per (query row, visible key, q head).
+    """
+    heads, kvh, dim, nseq, total, chunk = 32, 8, 128, 4, 4096, 512
+    nchunk = total // chunk
+    page = 64
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0002)
+    pool = pkg.KvCache(backend, kvh, dim, page, nseq * (total // page) + 8, total, nseq)
+    ids = [pool.open() for _ in range(nseq)]
+    gq = (1 + 0.02 * torch.randn(dim, generator=gen, device="cuda")).float()
+    gk = (1 + 0.02 * torch.randn(dim, generator=gen, device="cuda")).float()
+    rows = nseq * chunk
+    q = torch.randn((nchunk, rows, heads * dim), generator=gen, device="cuda").bfloat16()
+    k = torch.randn((nchunk, rows, kvh * dim), generator=gen, device="cuda").bfloat16()
+    v = torch.randn((nchunk, rows, kvh * dim), generator=gen, device="cuda").bfloat16()
+    out = torch.empty((rows, heads * dim), device="cuda")
+    positions = []
+    for c in range(nchunk):
+        p1 = torch.arange(c * chunk, (c + 1) * chunk, dtype=torch.int32, device="cuda")
+        positions.append(p1.repeat(nseq).view(rows, 1).repeat(1, 3).contiguous())
+
+    P = pkg.plugin
+    flags = (P.DEVICE_POINTERS | P.ASYNC | P.QK_NORM | P.INPUT_BF16 | P.MROPE_INTERLEAVED)
+    ids_c = (C.c_uint32 * nseq)(*ids)
+    rows_c = (C.c_uint32 * nseq)(*([chunk] * nseq))
+
+    def make_args(c):
+        a = P.AttentionArgs()
+        a.struct_size = C.sizeof(P.AttentionArgs)
+        a.flags = flags
+        a.heads, a.kv_heads, a.head_dim, a.rotary_dim = heads, kvh, dim, dim
+        a.eps, a.rope_theta = 1e-6, 1e6
+        a.num_seqs = nseq
+        a.seq_ids = ids_c
+        a.seq_rows = rows_c
+        a.q, a.k, a.v = q[c].data_ptr(), k[c].data_ptr(), v[c].data_ptr()
+        a.q_norm, a.k_norm = gq.data_ptr(), gk.data_ptr()
+        a.positions = positions[c].data_ptr()
+        a.out = out.data_ptr()
+        a.kv = pool.handle
+        return a
+
+    chunk_args = [make_args(c) for c in range(nchunk)]
+    fwd = backend.lib.safetyraise_kernel_attention_forward
+    ctx = backend.context
+
+    def chunk_flops(c):
+        # per (seq, q head): 4 * dim * sum_{i<512} (512 c + i + 1)
+        return 4 * dim * (chunk * chunk * c + chunk * (chunk + 1) // 2) * nseq * heads
+
+    step_flops = sum(chunk_flops(c) for c in range(nchunk))
+
+    def run_step(events=None):
+        for s in ids:
+            pool.truncate(s, 0)
+        for c in range(nchunk):
+            if events is not None:
+                events[c][0].record(stream)
+            st = fwd(ctx, C.byref(chunk_args[c]))
+            if events is not None:
+                events[c][1].record(stream)
+            if st != 0:
+                backend.check(st, "attention_forward")
+
+    for _ in range(warmup):
+        run_step()
+    backend.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(nchunk)] for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for s in range(steps):
+        run_step(ev[s])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / steps
+    tflops = step_flops / (ms_per_step * 1e-3) / 1e12
+    per_chunk_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev]).mean(0)
+    call_tflops = step_flops / (per_chunk_us.sum() * 1e-6) / 1e12
+    result = {
+        "workload": "qwen3-8b chunked causal prefill attention (BASELINE config 3): 4 x 4096 "
+                    "tokens in chunks of 512, one layer per step",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "pct_of_mfma_peak": round(100 * tflops / MFMA_BF16_PEAK_TFS, 2),
+        "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "gflop_per_step": round(step_flops / 1e9, 2),
+        "dtype": "bf16 MFMA, f32 accumulate and softmax",
+        "chunk_us": [round(float(x), 1) for x in per_chunk_us],
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(call_tflops, 2),
+            "peak": MFMA_BF16_PEAK_TFS,
+            "unit": "TFLOP/s",
+            "frac": round(call_tflops / MFMA_BF16_PEAK_TFS, 4),
+            "traffic": traffic_from_profiles("attn_prefill_qwen3_8b"),
+            "kernel": "kv_append_rows_kernel<128> + attn_prefill_kernel<128,4>",
+            "launch_us_mean": round(float(per_chunk_us.mean()), 2),
+            "flops_per_step": int(step_flops),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim,
+                                                      chunk)
+    pool.destroy()
+    backend.close()
+    return result
+
+
+def cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim, chunk):
+    """CPU oracle on a bounded sample: chunk 0 of sequence 0 (512 rows, empty cache)."""
+    from oracle import pyoracle as O
+
+    qn = q[0, :chunk].float().cpu().numpy()
+    kn = k[0, :chunk].float().cpu().numpy()
+    vn = v[0, :chunk].float().cpu().numpy()
+    pn = positions[0][:chunk].cpu().numpy().astype(np.int64)
+    gqn, gkn = gq.cpu().numpy(), gk.cpu().numpy()
+    flops = 4 * dim * (chunk * (chunk + 1) // 2) * heads
+    nthreads = min(os.cpu_count() or 1, 16)
+    res = {}
+    for threads in (1, nthreads):
+        cache = O.KvCache(kvh * dim, chunk, 64, bf16=True)
+        t = time.perf_counter()
+        O.attention_rows(qn, kn, vn, pn, cache, heads=heads, kv_heads=kvh, dim=dim,
+                         rotary_dim=dim, theta=1e6, eps=1e-6, q_norm=gqn, k_norm=gkn,
+                         threads=threads)
+        res[threads] = time.perf_counter() - t
+    return {
+        "value": round(flops / res[1] / 1e9, 3),
+        "unit": "GFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "chunk 0 of sequence 0 (512 rows on an empty cache, 32 heads) of the same "
+                  "inputs; f32 oracle with bf16 KV storage",
+        "ms": round(res[1] * 1e3, 1),
+        "all_cores": {"value": round(flops / res[nthreads] / 1e9, 3), "cores": nthreads,
+                      "ms": round(res[nthreads] * 1e3, 1)},
+    }
+
+
 def bench_copy(args, torch):
     """Calibration: a plain device copy of a known size (for PMC byte counters)."""
     nbytes = 1 << 30
@@ -287,6 +447,13 @@ def main():
     pkg = importlib.import_module("safetyraise-lmengine_amd")
     if args.workload == "decode":
         result = bench_decode(args, torch, pkg)
+        if not args.no_prefill:
+            result["prefill"] = bench_prefill(args, torch, pkg, args.prefill_steps, 2)
+    elif args.workload == "prefill":
+        result = bench_prefill(args, torch, pkg, args.steps, args.warmup)
+        result = {"metric": "prefill attn TFLOP/s, Qwen3-8B GQA shape", "n_gpus": 1,
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "data": "synthetic", "config": {"workload": result.pop("workload")}, **result}
     else:
         result = bench_copy(args, torch)
     print(json.dumps(result), flush=True)

@@ -22,6 +22,8 @@ namespace sr {
 namespace {
 
 constexpr size_t kAlign = 256;
+// Rows per sequence from which a call takes the chunked prefill kernels.
+constexpr uint32_t kPrefillMinRows = 16;
 
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
@@ -50,6 +52,12 @@ int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta
         }
         return kNoMemory;  // ensure_buffer already set the text
     }
+    return kOk;
+}
+
+int32_t run_prefill_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
+    const hipError_t e = launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size());
+    if (e != hipSuccess) return hip_fail(ctx, e, "prefill attention launch");
     return kOk;
 }
 
@@ -103,7 +111,6 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         return fail(ctx, kInvalid, "attention input or output pointer is NULL");
     }
     uint64_t total_rows = 0;
-    uint32_t max_rows = 0;
     std::vector<uint64_t> row0(A.num_seqs);
     for (uint32_t i = 0; i < A.num_seqs; ++i) {
         const uint32_t id = A.seq_ids[i];
@@ -119,7 +126,6 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         }
         row0[i] = total_rows;
         total_rows += A.seq_rows[i];
-        max_rows = std::max(max_rows, A.seq_rows[i]);
     }
     if (total_rows > INT32_MAX) return fail(ctx, kOverflow, "too many rows");
 
@@ -189,38 +195,98 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         if (st != kOk) return st;
     }
 
-    // Row r of every sequence with more than r rows: one decode step each, in
-    // row order, so row r sees the context plus rows 0..r (the reference
-    // appends then attends row by row, native.rs:637-638).
-    for (uint32_t r = 0; r < max_rows; ++r) {
+    // Sequences with at least kPrefillMinRows new rows take the chunked
+    // prefill kernels: all their rows are appended, then every row attends
+    // causally to the context plus the rows before it, in one launch pair.
+    std::vector<uint8_t> serial(A.num_seqs, 1);
+    uint32_t serial_rows = 0;
+    bool any_prefill = false;
+    const bool prefill_ok = prefill_supported(L);
+    {
         std::vector<SeqMeta> pack;
-        uint64_t pack_tokens = 0;
         for (uint32_t i = 0; i < A.num_seqs; ++i) {
-            if (A.seq_rows[i] <= r) continue;
+            if (!prefill_ok || A.seq_rows[i] < kPrefillMinRows) {
+                serial_rows = std::max(serial_rows, A.seq_rows[i]);
+                continue;
+            }
+            serial[i] = 0;
+            any_prefill = true;
             SeqMeta m{};
             m.slot = A.seq_ids[i];
-            m.ctx = (uint32_t)(old_len[i] + r);
-            m.rows = 1;
-            m.row0 = (uint32_t)(row0[i] + r);
-            if (!pack.empty() && pack_tokens + m.ctx + 1 > 0x7fffffffull) {
-                int32_t st = run_decode_pack(ctx, L, pack);
-                if (st != kOk) return st;
-                pack.clear();
-                pack_tokens = 0;
-            }
+            m.ctx = (uint32_t)old_len[i];
+            m.rows = A.seq_rows[i];
+            m.row0 = (uint32_t)row0[i];
             pack.push_back(m);
-            pack_tokens += (uint64_t)m.ctx + 1;
             if (pack.size() == (size_t)kMetaPerLaunch) {
-                int32_t st = run_decode_pack(ctx, L, pack);
+                int32_t st = run_prefill_pack(ctx, L, pack);
                 if (st != kOk) return st;
                 pack.clear();
-                pack_tokens = 0;
             }
         }
         if (!pack.empty()) {
-            int32_t st = run_decode_pack(ctx, L, pack);
+            int32_t st = run_prefill_pack(ctx, L, pack);
             if (st != kOk) return st;
         }
+    }
+
+    // Row r of every selected sequence with more than r rows: one decode step
+    // each, in row order, so row r sees the context plus rows 0..r (the
+    // reference appends then attends row by row, native.rs:637-638).
+    auto run_serial = [&](const std::vector<uint8_t> &which) -> int32_t {
+        uint32_t nrows = 0;
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            if (which[i]) nrows = std::max(nrows, A.seq_rows[i]);
+        }
+        for (uint32_t r = 0; r < nrows; ++r) {
+            std::vector<SeqMeta> pack;
+            uint64_t pack_tokens = 0;
+            for (uint32_t i = 0; i < A.num_seqs; ++i) {
+                if (!which[i] || A.seq_rows[i] <= r) continue;
+                SeqMeta m{};
+                m.slot = A.seq_ids[i];
+                m.ctx = (uint32_t)(old_len[i] + r);
+                m.rows = 1;
+                m.row0 = (uint32_t)(row0[i] + r);
+                if (!pack.empty() && pack_tokens + m.ctx + 1 > 0x7fffffffull) {
+                    int32_t st = run_decode_pack(ctx, L, pack);
+                    if (st != kOk) return st;
+                    pack.clear();
+                    pack_tokens = 0;
+                }
+                pack.push_back(m);
+                pack_tokens += (uint64_t)m.ctx + 1;
+                if (pack.size() == (size_t)kMetaPerLaunch) {
+                    int32_t st = run_decode_pack(ctx, L, pack);
+                    if (st != kOk) return st;
+                    pack.clear();
+                    pack_tokens = 0;
+                }
+            }
+            if (!pack.empty()) {
+                int32_t st = run_decode_pack(ctx, L, pack);
+                if (st != kOk) return st;
+            }
+        }
+        return kOk;
+    };
+    if (serial_rows > 0) {
+        int32_t st = run_serial(serial);
+        if (st != kOk) return st;
+    }
+    if (any_prefill && !async) {
+        // A synchronous call can recompute prefill rows whose MFMA operands
+        // left the fp16 range on the f32 split-K path (same cache positions,
+        // same values appended again).
+        uint32_t word = 0;
+        int32_t st = take_error_word(ctx, &word);
+        if (st == kOk && word == kErrPrefillRange) {
+            std::vector<uint8_t> redo(A.num_seqs);
+            for (uint32_t i = 0; i < A.num_seqs; ++i) redo[i] = serial[i] ? 0 : 1;
+            st = run_serial(redo);
+        } else if (st == kOk) {
+            st = error_word_status(ctx, word);
+        }
+        if (st != kOk) return st;
     }
     for (uint32_t i = 0; i < A.num_seqs; ++i) {
         pool->seqs[A.seq_ids[i]].len = old_len[i] + A.seq_rows[i];

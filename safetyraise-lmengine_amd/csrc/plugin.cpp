@@ -60,23 +60,40 @@ int32_t ensure_buffer(Ctx *ctx, DeviceBuffer &buf, size_t bytes, bool zero) {
     return kOk;
 }
 
+int32_t take_error_word(Ctx *ctx, uint32_t *word) {
+    SR_HIP(ctx, hipGetLastError());
+    SR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *word = 0;
+    SR_HIP(ctx, hipMemcpy(word, ctx->d_error_word, sizeof *word, hipMemcpyDeviceToHost));
+    if (*word != 0) {
+        uint32_t zero = 0;
+        SR_HIP(ctx, hipMemcpy(ctx->d_error_word, &zero, sizeof zero, hipMemcpyHostToDevice));
+    }
+    return kOk;
+}
+
+int32_t error_word_status(Ctx *ctx, uint32_t word) {
+    if (word == 0) return kOk;
+    if (word & kErrNonFiniteVariance) {
+        return fail(ctx, kInvalid, "RMSNorm variance is not finite (activation overflow)");
+    }
+    if (word & kErrNonFiniteKv) {
+        return fail(ctx, kInvalid, "KV append contains a non-finite value");
+    }
+    return fail(ctx, kInvalid,
+                "prefill attention met a K/V/q value outside the fp16 range of its MFMA "
+                "operands; repeat the call synchronously to recompute it on the f32 path");
+}
+
 int32_t finish_call(Ctx *ctx, bool async) {
     SR_HIP(ctx, hipGetLastError());
     if (async) {
         return kOk;
     }
-    SR_HIP(ctx, hipStreamSynchronize(ctx->stream));
     uint32_t word = 0;
-    SR_HIP(ctx, hipMemcpy(&word, ctx->d_error_word, sizeof word, hipMemcpyDeviceToHost));
-    if (word != 0) {
-        uint32_t zero = 0;
-        SR_HIP(ctx, hipMemcpy(ctx->d_error_word, &zero, sizeof zero, hipMemcpyHostToDevice));
-        if (word & kErrNonFiniteVariance) {
-            return fail(ctx, kInvalid, "RMSNorm variance is not finite (activation overflow)");
-        }
-        return fail(ctx, kInvalid, "KV append contains a non-finite value");
-    }
-    return kOk;
+    int32_t st = take_error_word(ctx, &word);
+    if (st != kOk) return st;
+    return error_word_status(ctx, word);
 }
 
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim) {

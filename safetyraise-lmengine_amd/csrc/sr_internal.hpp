@@ -24,6 +24,10 @@ constexpr int32_t kAbiMismatch = SAFETYRAISE_KERNEL_STATUS_ABI_MISMATCH;
 // Bits of the context's sticky device error word (set by kernels).
 constexpr uint32_t kErrNonFiniteKv = 1u;        // PagedKvCache::append rejects (state.rs:56-58)
 constexpr uint32_t kErrNonFiniteVariance = 2u;  // rms_norm rejects (math.rs:39-41)
+// A prefill row's output is not finite: some K, V or q value is outside the fp16
+// operand range of the MFMA prefill kernel; synchronous calls recompute on the
+// f32 split-K path.
+constexpr uint32_t kErrPrefillRange = 4u;
 
 // Sequences per kernel launch whose metadata travels in the kernel arguments.
 constexpr int kMetaPerLaunch = 64;
@@ -133,6 +137,10 @@ int32_t hip_fail(Ctx *ctx, hipError_t err, const char *what);
 bool checked_mul(uint64_t a, uint64_t b, uint64_t *out);
 int32_t ensure_buffer(Ctx *ctx, DeviceBuffer &buf, size_t bytes, bool zero);
 int32_t finish_call(Ctx *ctx, bool async);  // sync + sticky error check unless async
+// Synchronises the context stream and returns the sticky error word, cleared.
+int32_t take_error_word(Ctx *ctx, uint32_t *word);
+// The status and message for a non-zero error word.
+int32_t error_word_status(Ctx *ctx, uint32_t word);
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim);
 
 // KV pool helpers used by attention.
@@ -178,6 +186,12 @@ struct DecodePlanInput {
 // whose visible tokens sum below 2^31.
 hipError_t launch_attn_decode(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
                               const DecodePlanInput &in);
+
+// Chunked prefill: seqs[i].rows new rows appended after seqs[i].ctx cached
+// tokens, row i attending to ctx + i + 1 keys.  Up to kMetaPerLaunch
+// sequences; only for geometries where prefill_supported() holds.
+bool prefill_supported(const AttnLaunch &a);
+hipError_t launch_attn_prefill(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq);
 
 struct GdnLaunch {
     const safetyraise_kernel_gdn_pool *pool;
