@@ -155,8 +155,11 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_read(
  *          positions [rows][3] int32 (the three MRoPE axes; text uses p,p,p).
  * Output:  out [rows][heads*head_dim] f32.
  * seq_ids and seq_rows are always host arrays.  The kernel is chosen per
- * sequence: up to 16 rows go to the split-K decode/verify kernel, longer
- * chunks to the MFMA prefill kernel.
+ * sequence: fewer than 16 rows go to the split-K decode kernel (row by row),
+ * 16 or more to the MFMA prefill kernels.  A synchronous call whose prefill
+ * rows meet a K/V/q value beyond the fp16 range (|x| >= 65520) recomputes
+ * those sequences on the split-K path; an asynchronous one reports it at the
+ * next synchronous call.
  * ---------------------------------------------------------------------- */
 typedef struct safetyraise_kernel_attention_args {
     uint32_t struct_size;

@@ -56,7 +56,8 @@ int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta
 }
 
 int32_t run_prefill_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
-    const hipError_t e = launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size());
+    const hipError_t e =
+        launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size(), ctx->rope_scratch.ptr);
     if (e != hipSuccess) return hip_fail(ctx, e, "prefill attention launch");
     return kOk;
 }
@@ -189,9 +190,17 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     }
 
     std::vector<uint64_t> old_len(A.num_seqs);
-    for (uint32_t i = 0; i < A.num_seqs; ++i) {
-        old_len[i] = pool->seqs[A.seq_ids[i]].len;
-        int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i]);
+    {
+        TableBatch batch;  // one page-table upload for the whole call
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            old_len[i] = pool->seqs[A.seq_ids[i]].len;
+            int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i], &batch);
+            if (st != kOk) {
+                kv_flush_table(ctx, pool, batch);
+                return st;
+            }
+        }
+        int32_t st = kv_flush_table(ctx, pool, batch);
         if (st != kOk) return st;
     }
 
@@ -202,6 +211,10 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     uint32_t serial_rows = 0;
     bool any_prefill = false;
     const bool prefill_ok = prefill_supported(L);
+    if (prefill_ok) {
+        int32_t st = ensure_buffer(ctx, ctx->rope_scratch, prefill_rope_bytes(L, total_rows), false);
+        if (st != kOk) return st;
+    }
     {
         std::vector<SeqMeta> pack;
         for (uint32_t i = 0; i < A.num_seqs; ++i) {

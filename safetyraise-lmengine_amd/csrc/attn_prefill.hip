@@ -8,7 +8,9 @@
 // context plus rows 0..i (math.rs:102-155), and the Qwen3.5 output gate.
 //
 // Two kernels per launch:
-//   kv_append_rows_kernel  K RMSNorm + RoPE and V of every new row, rounded
+//   kv_append_rows_kernel  one workgroup per new row: the row's RoPE cos/sin
+//                          (once per rotary pair, also saved for the q side),
+//                          K RMSNorm + RoPE and V of every KV head, rounded
 //                          to bf16 into the pages (the reference appends
 //                          before it attends, so every row's keys must be in
 //                          the cache before any row attends);
@@ -22,6 +24,7 @@
 // transposed products every lane owns one query row: the row max needs a
 // single exchange between the two 32-lane halves (v_permlane32_swap), the row
 // sum stays lane-local until the end and rescaling O needs no shuffles.
+//
 // Operand precision.  The MFMAs run on fp16 operands: K and V tiles are the
 // cache's bf16 values converted exactly to fp16 while they are staged into
 // LDS (bf16 has fewer mantissa bits; every bf16 value of magnitude in
@@ -49,6 +52,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRowTile = 32;   // query rows per wave (the MFMA N dimension)
 constexpr int kKeyTile = 64;   // keys per LDS stage
+constexpr float kLazyRescale = 8.0f;
 
 struct PrefillMeta {
     uint32_t slot;  // page-table row
@@ -69,6 +73,7 @@ struct PrefillParams {
     const float *k_norm;
     const int32_t *positions;
     float *out;
+    float2 *rope_cs;  // [call rows][rotary_dim/2] (cos, sin), written by the append kernel
     uint32_t *err_word;
     uint64_t num_pages;
     uint32_t pages_per_seq;
@@ -85,7 +90,7 @@ struct PrefillParams {
     PrefillMeta meta[kMetaPerLaunch];
 };
 
-// Max of x over lanes l and l^32 (both halves get the same value).
+// Max / sum of x over lanes l and l^32 (both halves get the same bits).
 __device__ __forceinline__ float xhalf_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false,
                                                     false);
@@ -107,87 +112,122 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
 __device__ __forceinline__ float bf16_elem(const u32x4 &w, int e) {
     return (e & 1) ? bf16hi(w[e >> 1]) : bf16lo(w[e >> 1]);
 }
+// Materialises x in registers at this point of the program: register-only
+// work that produced x cannot be moved past it (for example across a
+// barrier into the next phase).
+template <typename T>
+__device__ __forceinline__ void pin(T &x) {
+    asm volatile("" : "+v"(x));
+}
+
+// Sum of the 8 fp16 values of x added to acc in f32 (v_dot2_f32_f16 with 1s).
+__device__ __forceinline__ float sum_f16x8(const f16x8 &x, float acc) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc = __builtin_amdgcn_fdot2(f16x2{x[2 * j], x[2 * j + 1]}, one, acc, false);
+    }
+    return acc;
+}
 
 // ---------------------------------------------------------------------------
-// K/V append of every new row: one wave per (row, KV head).
+// K/V append of every new row: one workgroup per row.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams p) {
     constexpr int EPL = D / 64;
-    __shared__ float rowbuf[4][D];
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
+    __shared__ float cs_s[128];
+    __shared__ float sn_s[128];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
     const PrefillMeta m = p.meta[blockIdx.y];
-    const uint32_t item = blockIdx.x * 4 + wave;
-    const bool valid = item < m.rows * p.kv_heads;
-    const uint32_t r = valid ? item / p.kv_heads : 0;
-    const uint32_t kvh = valid ? item % p.kv_heads : 0;
+    const uint32_t r = blockIdx.x;
+    if (r >= m.rows) return;
+    const uint32_t row = m.row0 + r;
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const bool interleaved = (p.flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
-    const size_t src = ((size_t)(m.row0 + r) * p.kv_heads + kvh) * D;
 
-    float x[EPL], vv[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        x[i] = valid ? load_act(p.k, src + lane + 64 * i, bf16_in) : 0.0f;
-        vv[i] = valid ? load_act(p.v, src + lane + 64 * i, bf16_in) : 0.0f;
+    // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with an IEEE
+    // f32 division (math.rs:90-91); once per row, shared with the q side
+    const uint32_t half = p.rotary_dim / 2;
+    if ((uint32_t)tid < half) {
+        const int32_t *pos3 = p.positions + (size_t)row * 3;
+        const int axis = rope_axis(tid, p.mrope, interleaved);
+        const float angle = (float)pos3[axis] / p.rope.denom[tid];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        cs_s[tid] = cs;
+        sn_s[tid] = sn;
+        p.rope_cs[(size_t)row * half + tid] = make_float2(cs, sn);
     }
-    if (qk_norm) {
-        // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
-        ss = sum64(ss);
-        const float variance = ss / (float)D;
-        if (valid && !isfinite(variance) && lane == 0) {
-            atomicOr(p.err_word, kErrNonFiniteVariance);
-        }
-        const float inv = 1.0f / sqrtf(variance + p.eps);
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (p.k_norm[lane + 64 * i] + norm_add);
-    }
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) rowbuf[wave][lane + 64 * i] = x[i];
     __syncthreads();
 
-    // RoPE, rotate-half over the first rotary_dim dims (math.rs:52-99)
-    const uint32_t half = p.rotary_dim / 2;
-    const int32_t *pos3 = p.positions + (size_t)(m.row0 + r) * 3;
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const uint32_t e = lane + 64 * i;
-        if (e < p.rotary_dim) {
-            const uint32_t pi = e < half ? e : e - half;
-            const int axis = rope_axis(pi, p.mrope, interleaved);
-            const float angle = (float)pos3[axis] / p.rope.denom[pi];
-            float sn, cs;
-            sincosf(angle, &sn, &cs);
-            const float left = rowbuf[wave][pi];
-            const float right = rowbuf[wave][pi + half];
-            x[i] = e < half ? left * cs - right * sn : right * cs + left * sn;
-        }
-    }
-    if (!valid) return;
     const uint32_t tok = m.ctx + r;
     const int32_t page = p.page_table[(size_t)m.slot * p.pages_per_seq + (tok >> p.log2_page_tokens)];
     const uint32_t pt_mask = (1u << p.log2_page_tokens) - 1;
-    const size_t dst = ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D;
     bool finite = true;
+    for (uint32_t kvh = wave; kvh < p.kv_heads; kvh += 4) {
+        const size_t src = ((size_t)row * p.kv_heads + kvh) * D;
+        float x[EPL], vv[EPL];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        finite = finite && isfinite(x[i]) && isfinite(vv[i]);
-        p.k_pages[dst + lane + 64 * i] = f32_to_bf16(x[i]);
-        p.v_pages[dst + lane + 64 * i] = f32_to_bf16(vv[i]);
+        for (int i = 0; i < EPL; ++i) {
+            x[i] = load_act(p.k, src + lane + 64 * i, bf16_in);
+            vv[i] = load_act(p.v, src + lane + 64 * i, bf16_in);
+        }
+        if (qk_norm) {
+            // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
+            ss = sum64(ss);
+            const float variance = ss / (float)D;
+            if (!isfinite(variance) && lane == 0) {
+                atomicOr(p.err_word, kErrNonFiniteVariance);
+            }
+            const float inv = 1.0f / sqrtf(variance + p.eps);
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (p.k_norm[lane + 64 * i] + norm_add);
+        }
+        // rotate-half over the first rotary_dim dims (math.rs:52-99): dim e
+        // pairs with e +- half, which lives in lane (e +- half) % 64
+        float y[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const uint32_t e = lane + 64 * i;
+            y[i] = x[i];
+            const uint32_t pe = e < half ? e + half : e - half;
+            float partner = 0.0f;
+#pragma unroll
+            for (int j = 0; j < EPL; ++j) {
+                const float t = __shfl(x[j], (int)(pe & 63));
+                if ((int)(pe >> 6) == j) partner = t;
+            }
+            if (e < p.rotary_dim) {
+                const uint32_t pi = e < half ? e : e - half;
+                y[i] = e < half ? x[i] * cs_s[pi] - partner * sn_s[pi]
+                                : x[i] * cs_s[pi] + partner * sn_s[pi];
+            }
+        }
+        const size_t dst =
+            ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            finite = finite && isfinite(y[i]) && isfinite(vv[i]);
+            p.k_pages[dst + lane + 64 * i] = f32_to_bf16(y[i]);
+            p.v_pages[dst + lane + 64 * i] = f32_to_bf16(vv[i]);
+        }
     }
     if (!finite) atomicOr(p.err_word, kErrNonFiniteKv);
 }
 
 // ---------------------------------------------------------------------------
 // Attention.  LDS per stage: K tile [64 keys][D] and V^T tile [D][64 keys],
-// both bf16, 16-byte units XOR-swizzled so that MFMA operand reads (eight
-// lanes on eight consecutive rows) and tile writes hit distinct banks.
+// both fp16, in 16-byte units XOR-swizzled so that MFMA operand reads (16
+// lanes on 16 consecutive rows) and tile writes spread over the banks with
+// 32 as well as with 64 four-byte banks.
 //
 // V^T column order.  The accumulator of S^T gives lane l (half h = l/32) the
 // keys 8a + 4h + b (a, b < 4) of each 32-key half tile.  The PV product takes
@@ -196,152 +236,197 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
 // step s is then one contiguous 16-byte read.
 // ---------------------------------------------------------------------------
 template <int D>
-struct PrefillLds {
-    static constexpr size_t kBytes = (size_t)kKeyTile * D * 2;  // one K or V^T tile
-    static constexpr size_t kStage = 2 * kBytes;
-    static constexpr size_t kTotal = 2 * kStage;  // double buffered
+constexpr size_t kTileBytes = (size_t)kKeyTile * D * 2;  // one K or V^T tile
+
+// 16-byte unit swizzles: K rows have D/8 units, V^T rows (64 keys) have 8.
+template <int D>
+__device__ __forceinline__ uint32_t k_swz(uint32_t key) {
+    return (D >= 128) ? (key & 15) : (key & 7);
+}
+__device__ __forceinline__ uint32_t vt_swz(uint32_t d) {
+    return ((d >> 1) & 7) ^ ((d & 1) << 2) ^ ((d >> 4) & 7);
+}
+
+// Where one workgroup's rows are: (sequence, KV head, row block) from the
+// block index, with the KV head fastest (the 8 XCDs take consecutive blocks,
+// so one KV head's blocks share an L2), then the sequence, then the row block
+// with the last (longest) blocks first.
+struct BlockPos {
+    PrefillMeta m;
+    uint32_t kvh;
+    uint32_t row0;    // first row of the block in the sequence
+    uint32_t n_keys;  // keys visible to the block's last row
+    uint32_t n_tiles;
+    bool active;
 };
-
-__device__ __forceinline__ uint32_t vt_swz(uint32_t d) { return (d & 7) ^ ((d >> 3) & 7); }
-
-// Two workgroups share a CU when the tiles fit twice in LDS (D <= 128): each
-// wave then gets at most 256 registers.
-template <int D, int G>
-__global__ __launch_bounds__(64 * G * ((G >= 4) ? 1 : (4 + G - 1) / G))
-__attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
-    const PrefillParams p) {
-    constexpr int R = (G >= 4) ? 1 : (4 + G - 1) / G;  // 32-row sub-blocks per workgroup
-    constexpr int NW = G * R;
-    constexpr int NTHR = 64 * NW;
-    constexpr int NS = D / 16;   // QK k-steps
-    constexpr int NT = D / 32;   // PV output tiles
-    constexpr int KCH = D / 8;   // 16-byte chunks per K row
-    constexpr int KL = (kKeyTile * KCH + NTHR - 1) / NTHR;
-    constexpr int VU = (kKeyTile / 4) * KCH;  // (4-key group, chunk) units of a V tile
-    constexpr int VL = (VU + NTHR - 1) / NTHR;
-    extern __shared__ __align__(16) unsigned char lds[];
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int h = lane >> 5;
-    const int col = lane & 31;
-
-    // blocks: KV head fastest (the 8 XCDs take consecutive blocks, so one KV
-    // head's blocks share an L2), then sequence, then row block, last first
-    const uint32_t b = blockIdx.x;
-    const uint32_t kvh = b % p.kv_heads;
-    const uint32_t t2 = b / p.kv_heads;
-    const uint32_t s = t2 % p.nseq;
-    const PrefillMeta m = p.meta[s];
+__device__ __forceinline__ BlockPos block_pos(const PrefillParams &p, uint32_t rows_per_block) {
+    BlockPos b;
+    const uint32_t t2 = blockIdx.x / p.kv_heads;
+    b.kvh = blockIdx.x % p.kv_heads;
+    b.m = p.meta[t2 % p.nseq];
     const uint32_t qb = p.max_blk - 1 - t2 / p.nseq;
-    if (qb >= m.nblk) return;
-    const uint32_t blk_row0 = qb * kRowTile * R;
-    const uint32_t blk_last = min(blk_row0 + kRowTile * R, m.rows) - 1;
-    const uint32_t n_keys = m.ctx + blk_last + 1;
-    const uint32_t n_tiles = (n_keys + kKeyTile - 1) / kKeyTile;
+    b.active = qb < b.m.nblk;
+    b.row0 = qb * rows_per_block;
+    const uint32_t last = min(b.row0 + rows_per_block, b.m.rows) - 1;
+    b.n_keys = b.m.ctx + last + 1;
+    b.n_tiles = (b.n_keys + kKeyTile - 1) / kKeyTile;
+    return b;
+}
 
-    const uint32_t head = kvh * G + (wave % G);
-    const uint32_t wrow0 = blk_row0 + kRowTile * (wave / G);
-    const uint32_t my_row = min(wrow0 + col, m.rows - 1);
-    const uint32_t key_limit = m.ctx + my_row;  // last visible key of this lane's row
+// Global -> register -> LDS movement of K and V tiles for a group of NTHR
+// threads (gt = thread index in the group).  K goes to LDS as fp16 [key][D]
+// (16-byte chunks), V as fp16 V^T (a thread owns 4 consecutive keys x 8 dims
+// and transposes them with the fp16 conversion).
+template <int D, int NTHR, bool kTilePage>
+struct TileIo {
+    static constexpr int KCH = D / 8;  // 16-byte chunks per K row
+    static constexpr int KL = (kKeyTile * KCH + NTHR - 1) / NTHR;
+    static constexpr int VU = (kKeyTile / 4) * KCH;  // (4-key group, chunk) units of a V tile
+    static constexpr int VL = (VU + NTHR - 1) / NTHR;
+    uint32_t k_goff[KL], k_loff[KL], v_goff[VL];
+    uint32_t v_loff[VL][8];
+    bool k_on[KL], v_on[VL];
+    const uint16_t *k_pages;
+    const uint16_t *v_pages;
+    const int32_t *table;
+    size_t head_base;
+    uint32_t lpt, pt_mask, n_keys, n_tiles;
 
-    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
-    const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
-    const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
-    const bool interleaved = (p.flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
-    const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
-
-    const int32_t *table = p.page_table + (size_t)m.slot * p.pages_per_seq;
-    const uint32_t lpt = p.log2_page_tokens;
-    const uint32_t pt_mask = (1u << lpt) - 1;
-    const size_t head_base = (size_t)kvh * p.num_pages;
-
-    auto tok_addr = [&](uint32_t tok) -> size_t {
+    __device__ __forceinline__ void init(int gt, const PrefillParams &p, const BlockPos &b) {
+        k_pages = p.k_pages;
+        v_pages = p.v_pages;
+        table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
+        head_base = (size_t)b.kvh * p.num_pages;
+        lpt = p.log2_page_tokens;
+        pt_mask = (1u << lpt) - 1;
+        n_keys = b.n_keys;
+        n_tiles = b.n_tiles;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const int c = gt + i * NTHR;
+            k_on[i] = (KL * NTHR == kKeyTile * KCH) || c < kKeyTile * KCH;
+            const int key = k_on[i] ? c / KCH : 0, ch = c % KCH;
+            k_goff[i] = key * D + ch * 8;
+            k_loff[i] = key * (D * 2) + ((ch ^ k_swz<D>(key)) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            const int u = gt + i * NTHR;
+            v_on[i] = (VL * NTHR == VU) || u < VU;
+            const int ch = u % KCH, g = v_on[i] ? u / KCH : 0;
+            const int sblk = g >> 2, q = g & 3;
+            const uint32_t unit = 2 * sblk + (q & 1);
+            v_goff[i] = 4 * g * D + ch * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = ch * 8 + e;
+                v_loff[i][e] = d * (kKeyTile * 2) + ((unit ^ vt_swz(d)) * 16) + 8 * (q >> 1);
+            }
+        }
+    }
+    // page id of tile t (tiles past the block clamp to its last tile)
+    __device__ __forceinline__ uint32_t page_of(uint32_t t) const {
+        return kTilePage ? (uint32_t)table[(min(t, n_tiles - 1) * kKeyTile) >> lpt] : 0u;
+    }
+    __device__ __forceinline__ size_t tok_addr(uint32_t tok) const {
         tok = min(tok, n_keys - 1);  // keys past the block's last row are masked
         return (((head_base + (uint32_t)table[tok >> lpt]) << lpt) + (tok & pt_mask)) * D;
-    };
-
-    u32x4 kreg[KL];
-    u32x4 vreg[VL][4];
-    auto load_tile = [&](u32x4(&kreg)[KL], u32x4(&vreg)[VL][4], uint32_t t) {
-        const uint32_t key0 = t * kKeyTile;
+    }
+    __device__ __forceinline__ size_t tile_base(uint32_t t, uint32_t pg) const {
+        return (((head_base + pg) << lpt) + ((t * kKeyTile) & pt_mask)) * D;
+    }
+    template <int N>
+    __device__ __forceinline__ void load_k(u32x4 (&r)[N], uint32_t t, uint32_t pg) const {
+        static_assert(N >= KL, "staging registers");
+        const uint16_t *kb = k_pages + tile_base(t, pg);
 #pragma unroll
         for (int i = 0; i < KL; ++i) {
-            const int c = tid + i * NTHR;
-            if ((KL * NTHR == kKeyTile * KCH) || c < kKeyTile * KCH) {
-                const int key = c / KCH, ch = c % KCH;
-                kreg[i] = *(const u32x4 *)(p.k_pages + tok_addr(key0 + key) + ch * 8);
+            if (!k_on[i]) continue;
+            if constexpr (kTilePage) {
+                r[i] = *(const u32x4 *)(kb + k_goff[i]);
+            } else {
+                r[i] = *(const u32x4 *)(k_pages + tok_addr(t * kKeyTile + k_goff[i] / D) +
+                                        k_goff[i] % D);
             }
         }
+    }
+    template <int N>
+    __device__ __forceinline__ void load_v(u32x4 (&r)[N], uint32_t t, uint32_t pg) const {
+        static_assert(N >= 4 * VL, "staging registers");
+        const uint16_t *vb = v_pages + tile_base(t, pg);
 #pragma unroll
         for (int i = 0; i < VL; ++i) {
-            const int u = tid + i * NTHR;
-            if ((VL * NTHR == VU) || u < VU) {
-                const int ch = u % KCH, g = u / KCH;
+            if (!v_on[i]) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (kTilePage) {
+                    r[4 * i + j] = *(const u32x4 *)(vb + v_goff[i] + j * D);
+                } else {
+                    r[4 * i + j] = *(const u32x4 *)(
+                        v_pages + tok_addr(t * kKeyTile + v_goff[i] / D + j) + v_goff[i] % D);
+                }
+            }
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void store_k(const u32x4 (&r)[N], unsigned char *kt) const {
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            if (!k_on[i]) continue;
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(r[i][j]), bf16hi(r[i][j]));
+            *(u32x4 *)(kt + k_loff[i]) = f;
+        }
+    }
+    // valid_keys: keys of the tile that exist; the rest may hold any bits
+    // (pages are reused), and although their P is 0, 0 * NaN is not, so in
+    // the last tile they become 0.
+    template <int N>
+    __device__ __forceinline__ void store_v(const u32x4 (&r)[N], unsigned char *vt,
+                                            uint32_t valid_keys) const {
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            if (!v_on[i]) continue;
+            u32x4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = r[4 * i + j];
+            if (valid_keys < (uint32_t)kKeyTile) {
+                const uint32_t key = v_goff[i] / D;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    vreg[i][j] = *(const u32x4 *)(p.v_pages + tok_addr(key0 + 4 * g + j) + ch * 8);
+                    if (key + j >= valid_keys) w[j] = u32x4{0, 0, 0, 0};
                 }
             }
-        }
-    };
-    auto store_tile = [&](const u32x4(&kreg)[KL], const u32x4(&vreg)[VL][4], int buf) {
-        unsigned char *kt = lds + buf * PrefillLds<D>::kStage;
-        unsigned char *vt = kt + PrefillLds<D>::kBytes;
 #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-            const int c = tid + i * NTHR;
-            if ((KL * NTHR == kKeyTile * KCH) || c < kKeyTile * KCH) {
-                const int key = c / KCH, ch = c % KCH;
-                const u32x4 w = kreg[i];
-                u32x4 f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(w[j]), bf16hi(w[j]));
-                *(u32x4 *)(kt + key * (D * 2) + ((ch ^ (key & 7)) * 16)) = f;
+            for (int e = 0; e < 8; ++e) {
+                // dim ch*8 + e of the 4 keys, as two fp16 pairs
+                const uint32_t lo = pack_f16x2(bf16_elem(w[0], e), bf16_elem(w[1], e));
+                const uint32_t hi = pack_f16x2(bf16_elem(w[2], e), bf16_elem(w[3], e));
+                *(uint2 *)(vt + v_loff[i][e]) = make_uint2(lo, hi);
             }
         }
-#pragma unroll
-        for (int i = 0; i < VL; ++i) {
-            const int u = tid + i * NTHR;
-            if ((VL * NTHR == VU) || u < VU) {
-                const int ch = u % KCH, g = u / KCH;
-                const int sblk = g >> 2, q = g & 3;
-                const uint32_t unit = 2 * sblk + (q & 1);
-                const uint32_t byte_in = 8 * (q >> 1);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    // dim ch*8 + e of the 4 keys, as two fp16 pairs
-                    const uint32_t lo =
-                        pack_f16x2(bf16_elem(vreg[i][0], e), bf16_elem(vreg[i][1], e));
-                    const uint32_t hi =
-                        pack_f16x2(bf16_elem(vreg[i][2], e), bf16_elem(vreg[i][3], e));
-                    const uint32_t d = ch * 8 + e;
-                    *(uint2 *)(vt + d * (kKeyTile * 2) + ((unit ^ vt_swz(d)) * 16) + byte_in) =
-                        make_uint2(lo, hi);
-                }
-            }
-        }
-    };
+    }
+};
 
-    // tile 0 is requested before the q prologue so its latency overlaps it
-    load_tile(kreg, vreg, 0);
-
-    // ---- q: RMSNorm, RoPE, scale, fp16 (lane holds dims 16s + 8h + j) ----
-    const uint32_t hs = gated ? 2 * D : D;
-    const size_t qbase = (size_t)(m.row0 + my_row) * p.heads * hs + (size_t)head * hs;
+// One wave's query rows: q RMSNorm (math.rs:28-50), RoPE with the row's
+// cos/sin from the append kernel, scale by log2(e)/sqrt(D), fp16.  The lane
+// holds row (row0 + col) and dims 16s + 8h + j (the B operand of S^T).
+template <int D>
+__device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase, uint32_t call_row,
+                                           int h, int lane, f16x8 (&qop)[D / 16]) {
+    constexpr int NS = D / 16;
+    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
+    const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
     float x[NS][8];
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
         const size_t off = qbase + 16 * st + 8 * h;
         if (bf16_in) {
-            const uint4 w = *(const uint4 *)((const uint16_t *)p.q + off);
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            const u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + off);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[st][2 * j] = bf16lo(ww[j]);
-                x[st][2 * j + 1] = bf16hi(ww[j]);
-            }
+            for (int j = 0; j < 8; ++j) x[st][j] = bf16_elem(w, j);
         } else {
             const float4 a = *(const float4 *)((const float *)p.q + off);
             const float4 c = *(const float4 *)((const float *)p.q + off + 4);
@@ -370,49 +455,48 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
             for (int j = 0; j < 8; ++j) x[st][j] = x[st][j] * inv * (wv[j] + norm_add);
         }
     }
-    {
-        // pairs (i, i + rotary_dim/2); the host routes only rotary_dim/2 that
-        // is a multiple of 16 here, so both halves of a pair sit in this lane
-        const uint32_t hsteps = p.rotary_dim / 32;
-        const int32_t *pos3 = p.positions + (size_t)(m.row0 + my_row) * 3;
-        const int32_t pos0 = pos3[0], pos1 = pos3[1], pos2 = pos3[2];
-        // (the partner step st + hsteps is selected with compile-time indices
-        // so that x stays in registers)
+    // pairs (i, i + rotary_dim/2); the host routes only rotary_dim/2 that is
+    // a multiple of 16 here, so both halves of a pair sit in this lane (the
+    // partner step st + hsteps is selected with compile-time indices so that
+    // x stays in registers)
+    const uint32_t half = p.rotary_dim / 2;
+    const uint32_t hsteps = p.rotary_dim / 32;
+    const float2 *cs_row = p.rope_cs + (size_t)call_row * half;
 #pragma unroll
-        for (int st = 0; st < NS / 2; ++st) {
-            if ((uint32_t)st < hsteps) {
-                float right[8];
+    for (int st = 0; st < NS / 2; ++st) {
+        if ((uint32_t)st < hsteps) {
+            float right[8];
 #pragma unroll
-                for (int k = 1; k <= NS / 2; ++k) {
-                    if ((uint32_t)k == hsteps) {
+            for (int k = 1; k <= NS / 2; ++k) {
+                if ((uint32_t)k == hsteps) {
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) right[j] = x[st + k][j];
-                    }
+                    for (int j = 0; j < 8; ++j) right[j] = x[st + k][j];
                 }
+            }
+            const float4 *c4 = (const float4 *)(cs_row + 16 * st + 8 * h);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t i = 16 * st + 8 * h + j;
-                    const int axis = rope_axis(i, p.mrope, interleaved);
-                    const int32_t pa = axis == 0 ? pos0 : (axis == 1 ? pos1 : pos2);
-                    const float angle = (float)pa / p.rope.denom[i];
-                    float sn, cs;
-                    sincosf(angle, &sn, &cs);
+            for (int j2 = 0; j2 < 4; ++j2) {
+                const float4 cc = c4[j2];  // (cos, sin) of pairs 2*j2 and 2*j2 + 1
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int j = 2 * j2 + k;
+                    const float cs = k ? cc.z : cc.x;
+                    const float sn = k ? cc.w : cc.y;
                     const float left = x[st][j];
                     x[st][j] = left * cs - right[j] * sn;
                     right[j] = right[j] * cs + left * sn;
                 }
+            }
 #pragma unroll
-                for (int k = 1; k <= NS / 2; ++k) {
-                    if ((uint32_t)k == hsteps) {
+            for (int k = 1; k <= NS / 2; ++k) {
+                if ((uint32_t)k == hsteps) {
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) x[st + k][j] = right[j];
-                    }
+                    for (int j = 0; j < 8; ++j) x[st + k][j] = right[j];
                 }
             }
         }
     }
     const float qscale = (1.0f / sqrtf((float)D)) * kLog2e;
-    f16x8 qop[NS];
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
         f32x8 v;
@@ -420,97 +504,117 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
         for (int j = 0; j < 8; ++j) v[j] = x[st][j] * qscale;
         qop[st] = __builtin_convertvector(v, f16x8);
     }
+}
 
-    // ---- main loop over 64-key tiles ----
-    f32x16 oacc[NT];
+// S^T = K Q^T for the 64 keys of a tile (two 32-key accumulators, operands
+// read two k-steps ahead of their MFMA).
+template <int D>
+__device__ __forceinline__ void s_tile(const unsigned char *kt, const f16x8 (&qop)[D / 16], int h,
+                                       int col, f32x16 (&sacc)[2]) {
+    constexpr int NS = D / 16;
+    auto k_frag = [&](int u, int st) -> f16x8 {
+        const int key = 32 * u + col;
+        return *(const f16x8 *)(kt + key * (D * 2) + (((2 * st + h) ^ k_swz<D>(key)) * 16));
+    };
+    sacc[0] = f32x16{};
+    sacc[1] = f32x16{};
+    f16x8 ka[2][2] = {{k_frag(0, 0), k_frag(1, 0)}, {k_frag(0, 1), k_frag(1, 1)}};
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
-    const uint32_t first_row_limit = m.ctx + blk_row0;  // smallest key limit in the block
-
-    for (uint32_t t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
-        store_tile(kreg, vreg, buf);
-        __syncthreads();
-        if (t + 1 < n_tiles) load_tile(kreg, vreg, t + 1);
-        const unsigned char *kt = lds + buf * PrefillLds<D>::kStage;
-        const unsigned char *vt = kt + PrefillLds<D>::kBytes;
-
-        // S^T = K Q^T for keys [32u, 32u + 32) of the tile
-        f32x16 sacc[2];
+    for (int st = 0; st < NS; ++st) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            sacc[u] = f32x16{};
-            const int key = 32 * u + col;
-#pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                const f16x8 a =
-                    *(const f16x8 *)(kt + key * (D * 2) + (((2 * st + h) ^ (key & 7)) * 16));
-                sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qop[st], sacc[u], 0, 0, 0);
-            }
+            sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 1][u], qop[st], sacc[u], 0, 0,
+                                                             0);
+            if (st + 2 < NS) ka[st & 1][u] = k_frag(u, st + 2);
         }
-        const uint32_t key0 = t * kKeyTile;
-        if (key0 + kKeyTile - 1 > first_row_limit) {
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// O^T += V^T P^T (operands read one k-step ahead of their MFMA).
+template <int D>
+__device__ __forceinline__ void pv_tile(const unsigned char *vt, const f16x8 (&pop)[4], int h,
+                                        int col, f32x16 (&oacc)[D / 32]) {
+    constexpr int NT = D / 32;
+    auto v_frag = [&](int tt, int st) -> f16x8 {
+        const uint32_t d = 32 * tt + col;
+        return *(const f16x8 *)(vt + d * (kKeyTile * 2) + (((2 * st + h) ^ vt_swz(d)) * 16));
+    };
+    f16x8 va[2][NT];
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+    for (int tt = 0; tt < NT; ++tt) va[0][tt] = v_frag(tt, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
-                    if (key > key_limit) sacc[u][i] = -INFINITY;
-                }
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            if (st + 1 < 4) va[(st + 1) & 1][tt] = v_frag(tt, st + 1);
+            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[st & 1][tt], pop[st], oacc[tt], 0,
+                                                              0, 0);
         }
-        float mx = sacc[0][0];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[u][i]);
-        mx = xhalf_max(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        float psum = 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Online softmax of one tile (math.rs:133-148 in the log2 domain): causal
+// mask, row max across the two lane halves, P = 2^(s - m) in fp16, row sum of
+// those fp16 values, lazy rescale of O (only when some row's max moved).
+template <int D>
+__device__ __forceinline__ void softmax_tile(f32x16 (&sacc)[2], uint32_t key0, bool masked,
+                                             uint32_t key_limit, int h, float &m_run, float &l_run,
+                                             f32x16 (&oacc)[D / 32], f16x8 (&pop)[4]) {
+    constexpr int NT = D / 32;
+    if (masked) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float pv = fast_exp2(sacc[u][i] - m_new);
-                sacc[u][i] = pv;
-                psum += pv;
+                const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (key > key_limit) sacc[u][i] = -INFINITY;
             }
-        l_run = l_run * alpha + psum;
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-            for (int tt = 0; tt < NT; ++tt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[tt][i] *= alpha;
-        }
-        f16x8 pop[4];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            f32x8 v;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = sacc[st >> 1][8 * (st & 1) + j];
-            pop[st] = __builtin_convertvector(v, f16x8);
-        }
-        // O^T += V^T P^T
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            const uint32_t d = 32 * tt + col;
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const f16x8 a = *(const f16x8 *)(vt + d * (kKeyTile * 2) +
-                                                   (((2 * st + h) ^ vt_swz(d)) * 16));
-                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pop[st], oacc[tt], 0, 0, 0);
-            }
-        }
     }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[u][i]);
+    mx = xhalf_max(mx);
+    // the reference max is only raised when it grows by more than
+    // kLazyRescale (log2 units): P stays <= 2^kLazyRescale (exact range for
+    // fp16) and O is rescaled rarely; o / l is the same for any common shift
+    const float m_new = (mx > m_run + kLazyRescale) ? mx : m_run;
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        f32x8 v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = fast_exp2(sacc[st >> 1][8 * (st & 1) + j] - m_new);
+        pop[st] = __builtin_convertvector(v, f16x8);
+    }
+    // the row sum uses the fp16 probabilities the PV product uses
+    const float lt =
+        sum_f16x8(pop[0], sum_f16x8(pop[2], 0.0f)) + sum_f16x8(pop[1], sum_f16x8(pop[3], 0.0f));
+    l_run = l_run * alpha + lt;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[tt][i] *= alpha;
+    }
+}
 
-    // ---- epilogue: o / l, Qwen3.5 gate, f32 store ----
-    const uint32_t row = wrow0 + col;
-    if (row >= m.rows) return;
-    const float inv_l = 1.0f / xhalf_sum(l_run);
-    float *dst = p.out + (size_t)(m.row0 + row) * p.heads * D + (size_t)head * D;
+// o / l, Qwen3.5 gate (math.rs sigmoid), f32 store; flags non-finite rows.
+template <int D>
+__device__ __forceinline__ void store_rows(const PrefillParams &p, uint32_t call_row, uint32_t head,
+                                           size_t qbase, int h, float l_run,
+                                           const f32x16 (&oacc)[D / 32]) {
+    constexpr int NT = D / 32;
+    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
+    const float inv_l = 1.0f / l_run;
+    float *dst = p.out + (size_t)call_row * p.heads * D + (size_t)head * D;
     bool finite = true;
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
@@ -535,43 +639,278 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
     if (!finite) atomicOr(p.err_word, kErrPrefillRange);
 }
 
-template <int D, int G>
-hipError_t launch_dg(hipStream_t stream, const PrefillParams &p, uint32_t append_blocks_x) {
-    constexpr int R = (G >= 4) ? 1 : (4 + G - 1) / G;
-    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3(append_blocks_x, p.nseq), dim3(256), 0,
-                       stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    static bool configured = false;
-    const size_t lds = PrefillLds<D>::kTotal;
-    if (!configured) {
-        e = hipFuncSetAttribute((const void *)attn_prefill_kernel<D, G>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        configured = true;
+// ---------------------------------------------------------------------------
+// attn_prefill_kernel: all waves of a workgroup process every tile in step
+// (one barrier per tile).  One workgroup = the G heads of a KV group x R
+// blocks of 32 rows; two workgroups share a CU when the tiles fit twice in
+// LDS (D <= 128), each wave then gets at most 256 registers.  Used where the
+// ping-pong kernel below does not apply.
+// kTilePage: page_tokens >= 64, so a 64-key tile lies in one page and its
+// address is one wave-uniform page lookup plus per-thread constants.
+// ---------------------------------------------------------------------------
+template <int G>
+constexpr int kLockstepRows = (G >= 4) ? 1 : (4 + G - 1) / G;
+
+template <int D, int G, bool kTilePage>
+__global__ __launch_bounds__(64 * G * kLockstepRows<G>)
+__attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
+    const PrefillParams p) {
+    constexpr int R = kLockstepRows<G>;
+    constexpr int NTHR = 64 * G * R;
+    constexpr int NS = D / 16;
+    constexpr int NT = D / 32;
+    using Io = TileIo<D, NTHR, kTilePage>;
+    extern __shared__ __align__(16) unsigned char lds[];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const BlockPos b = block_pos(p, kRowTile * R);
+    if (!b.active) return;
+    const uint32_t head = b.kvh * G + (wave % G);
+    const uint32_t wrow0 = b.row0 + kRowTile * (wave / G);
+    const uint32_t my_row = min(wrow0 + col, b.m.rows - 1);
+    const uint32_t key_limit = b.m.ctx + my_row;  // last visible key of this lane's row
+    const uint32_t first_row_limit = b.m.ctx + b.row0;
+    const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
+    const size_t qbase = (size_t)(b.m.row0 + my_row) * p.heads * hs + (size_t)head * hs;
+
+    Io io;
+    io.init(tid, p, b);
+    u32x4 kreg[Io::KL];
+    u32x4 vreg[4 * Io::VL];
+    uint32_t pg_next = io.page_of(1);
+    {
+        const uint32_t pg0 = io.page_of(0);
+        io.load_k(kreg, 0, pg0);  // before the q prologue, so their latency overlaps it
+        io.load_v(vreg, 0, pg0);
     }
-    const uint32_t blocks = p.max_blk * p.nseq * p.kv_heads;
-    hipLaunchKernelGGL((attn_prefill_kernel<D, G>), dim3(blocks), dim3(64 * G * R), lds, stream,
-                       p);
+    f16x8 qop[NS];
+    q_operands<D>(p, qbase, b.m.row0 + my_row, h, lane, qop);
+
+    f32x16 oacc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    for (uint32_t t = 0; t < b.n_tiles; ++t) {
+        unsigned char *kt = lds + (t & 1) * 2 * kTileBytes<D>;
+        unsigned char *vt = kt + kTileBytes<D>;
+        const uint32_t key0 = t * kKeyTile;
+        io.store_k(kreg, kt);
+        io.store_v(vreg, vt, b.n_keys - key0);
+        __syncthreads();
+        if (t + 1 < b.n_tiles) {
+            const uint32_t pg = pg_next;
+            pg_next = io.page_of(t + 2);  // read two tiles ahead
+            io.load_k(kreg, t + 1, pg);
+            io.load_v(vreg, t + 1, pg);
+        }
+        f32x16 sacc[2];
+        s_tile<D>(kt, qop, h, col, sacc);
+        f16x8 pop[4];
+        softmax_tile<D>(sacc, key0, key0 + kKeyTile - 1 > first_row_limit, key_limit, h, m_run,
+                        l_run, oacc, pop);
+        pv_tile<D>(vt, pop, h, col, oacc);
+    }
+    const uint32_t row = wrow0 + col;
+    const float l = xhalf_sum(l_run);
+    if (row < b.m.rows) store_rows<D>(p, b.m.row0 + row, head, qbase, h, l, oacc);
+}
+
+// ---------------------------------------------------------------------------
+// attn_prefill_pp_kernel: two groups of 4 waves, one wave of each on every
+// SIMD, run half an iteration apart ("ping-pong").  The barriers of the
+// workgroup split time into phases; in each phase one group issues MFMAs
+// (PV of tile t-1 and S of tile t) while the other runs VALU work (softmax
+// of its tile t and the staging of the next tile), so each SIMD's matrix
+// unit is fed by one wave while its vector unit is busy with the other.
+//
+//   phase    2t        2t+1        2t+2
+//   group 0  M(t)      V(t)        M(t+1)
+//   group 1  V(t-1)    M(t)        V(t)
+//
+// Group 0 converts and stores K tiles, group 1 V tiles, each loading its next
+// tile into registers two phases ahead.  K(t) is read in phases 2t and 2t+1
+// and K(t+2) written in phase 2t+3: two K buffers.  V(t) is read in phases
+// 2t+2 and 2t+3 while V(t+2) is written in phase 2t+2: three V buffers.
+// Every wave passes the same number of barriers (group 1 one extra at the
+// start, group 0 one extra at the end).
+// One workgroup = 2 x 4 waves = (G heads x 4/G blocks of 32 rows) per group.
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr size_t kPingPongLds = 5 * kTileBytes<D>;  // K x 2, V x 3
+
+template <int D, int G, bool kTilePage>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void
+attn_prefill_pp_kernel(const PrefillParams p) {
+    constexpr int RG = 4 / G;  // row blocks per group
+    constexpr int NS = D / 16;
+    constexpr int NT = D / 32;
+    using Io = TileIo<D, 256, kTilePage>;
+    constexpr int SL = (Io::KL > 4 * Io::VL) ? Io::KL : 4 * Io::VL;
+    extern __shared__ __align__(16) unsigned char lds[];
+    unsigned char *kbuf = lds;                         // 2 K tiles
+    unsigned char *vbuf = lds + 2 * kTileBytes<D>;     // 3 V^T tiles
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const int grp = wave >> 2;  // waves w and w + 4 share a SIMD
+    const int gw = wave & 3;
+    const BlockPos b = block_pos(p, 2 * kRowTile * RG);
+    if (!b.active) return;
+    const uint32_t head = b.kvh * G + (gw % G);
+    const uint32_t wrow0 = b.row0 + kRowTile * (grp * RG + gw / G);
+    const uint32_t my_row = min(wrow0 + col, b.m.rows - 1);
+    const uint32_t key_limit = b.m.ctx + my_row;
+    const uint32_t first_row_limit = b.m.ctx + b.row0;
+    const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
+    const size_t qbase = (size_t)(b.m.row0 + my_row) * p.heads * hs + (size_t)head * hs;
+    const uint32_t n = b.n_tiles;
+
+    Io io;
+    io.init(tid & 255, p, b);
+    u32x4 stage[SL];
+    // tile 0: K by group 0, V by group 1; then each group's tile 1 in flight
+    {
+        const uint32_t pg0 = io.page_of(0);
+        if (grp == 0) io.load_k(stage, 0, pg0);
+        else io.load_v(stage, 0, pg0);
+    }
+    f16x8 qop[NS];
+    q_operands<D>(p, qbase, b.m.row0 + my_row, h, lane, qop);
+    if (grp == 0) io.store_k(stage, kbuf);
+    else io.store_v(stage, vbuf, b.n_keys);
+    uint32_t pg_next = io.page_of(2);
+    if (n > 1) {
+        const uint32_t pg1 = io.page_of(1);
+        if (grp == 0) io.load_k(stage, 1, pg1);
+        else io.load_v(stage, 1, pg1);
+    }
+    f32x16 oacc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    f16x8 pop[4];
+    __syncthreads();
+    if (grp == 1) __syncthreads();  // group 1 starts one phase later
+
+    for (uint32_t t = 0; t < n; ++t) {
+        // ---- M phase: PV(t-1), S(t) ----
+        if (t > 0) pv_tile<D>(vbuf + ((t - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
+        f32x16 sacc[2];
+        s_tile<D>(kbuf + (t & 1) * kTileBytes<D>, qop, h, col, sacc);
+        __syncthreads();
+        // ---- V phase: softmax(t), stage the group's tile t+1, load t+2 ----
+        const uint32_t key0 = t * kKeyTile;
+        softmax_tile<D>(sacc, key0, key0 + kKeyTile - 1 > first_row_limit, key_limit, h, m_run,
+                        l_run, oacc, pop);
+        if (t + 1 < n) {
+            if (grp == 0) io.store_k(stage, kbuf + ((t + 1) & 1) * kTileBytes<D>);
+            else io.store_v(stage, vbuf + ((t + 1) % 3) * kTileBytes<D>, b.n_keys - key0 - kKeyTile);
+            if (t + 2 < n) {
+                const uint32_t pg = pg_next;
+                pg_next = io.page_of(t + 3);
+                if (grp == 0) io.load_k(stage, t + 2, pg);
+                else io.load_v(stage, t + 2, pg);
+            }
+        }
+        // the softmax results stay in this phase
+#pragma unroll
+        for (int st = 0; st < 4; ++st) pin(pop[st]);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) pin(oacc[tt]);
+        __syncthreads();
+    }
+    pv_tile<D>(vbuf + ((n - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
+    if (grp == 0) __syncthreads();  // matches group 1's extra barrier
+
+    const uint32_t row = wrow0 + col;
+    const float l = xhalf_sum(l_run);
+    if (row < b.m.rows) store_rows<D>(p, b.m.row0 + row, head, qbase, h, l, oacc);
+}
+
+template <int D, int G>
+constexpr bool kUsePingPong = (D <= 128) && (G == 1 || G == 2 || G == 4);
+
+template <int D, int G>
+uint32_t rows_per_block_dg() {
+    return kUsePingPong<D, G> ? 2 * kRowTile * (4 / G) : kRowTile * kLockstepRows<G>;
+}
+
+template <int D, int G, bool kTilePage>
+hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t blocks) {
+    static bool configured = false;
+    if constexpr (kUsePingPong<D, G>) {
+        const size_t lds = kPingPongLds<D>;
+        if (!configured) {
+            const hipError_t e =
+                hipFuncSetAttribute((const void *)attn_prefill_pp_kernel<D, G, kTilePage>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            configured = true;
+        }
+        hipLaunchKernelGGL((attn_prefill_pp_kernel<D, G, kTilePage>), dim3(blocks), dim3(512), lds,
+                           stream, p);
+    } else {
+        const size_t lds = 4 * kTileBytes<D>;  // K and V^T, double buffered
+        if (!configured) {
+            const hipError_t e =
+                hipFuncSetAttribute((const void *)attn_prefill_kernel<D, G, kTilePage>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            configured = true;
+        }
+        hipLaunchKernelGGL((attn_prefill_kernel<D, G, kTilePage>), dim3(blocks),
+                           dim3(64 * G * kLockstepRows<G>), lds, stream, p);
+    }
     return hipGetLastError();
 }
 
+template <int D, int G>
+hipError_t launch_dg(hipStream_t stream, PrefillParams &p, const SeqMeta *seqs, int nseq) {
+    const uint32_t rpb = rows_per_block_dg<D, G>();
+    uint32_t max_blk = 0, max_rows = 0;
+    for (int i = 0; i < nseq; ++i) {
+        PrefillMeta &m = p.meta[i];
+        m.slot = seqs[i].slot;
+        m.ctx = seqs[i].ctx;
+        m.rows = seqs[i].rows;
+        m.row0 = seqs[i].row0;
+        m.nblk = (m.rows + rpb - 1) / rpb;
+        max_blk = std::max(max_blk, m.nblk);
+        max_rows = std::max(max_rows, m.rows);
+    }
+    p.max_blk = max_blk;
+    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3(max_rows, p.nseq), dim3(256), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t blocks = p.max_blk * p.nseq * p.kv_heads;
+    if (p.log2_page_tokens >= 6) return launch_attn<D, G, true>(stream, p, blocks);
+    return launch_attn<D, G, false>(stream, p, blocks);
+}
+
 template <int D>
-hipError_t launch_d(hipStream_t stream, const PrefillParams &p, uint32_t g, uint32_t ax) {
+hipError_t launch_d(hipStream_t stream, PrefillParams &p, uint32_t g, const SeqMeta *seqs,
+                    int nseq) {
     switch (g) {
-        case 1: return launch_dg<D, 1>(stream, p, ax);
-        case 2: return launch_dg<D, 2>(stream, p, ax);
-        case 3: return launch_dg<D, 3>(stream, p, ax);
-        case 4: return launch_dg<D, 4>(stream, p, ax);
-        case 5: return launch_dg<D, 5>(stream, p, ax);
-        case 6: return launch_dg<D, 6>(stream, p, ax);
-        case 7: return launch_dg<D, 7>(stream, p, ax);
-        case 8: return launch_dg<D, 8>(stream, p, ax);
+        case 1: return launch_dg<D, 1>(stream, p, seqs, nseq);
+        case 2: return launch_dg<D, 2>(stream, p, seqs, nseq);
+        case 3: return launch_dg<D, 3>(stream, p, seqs, nseq);
+        case 4: return launch_dg<D, 4>(stream, p, seqs, nseq);
+        case 5: return launch_dg<D, 5>(stream, p, seqs, nseq);
+        case 6: return launch_dg<D, 6>(stream, p, seqs, nseq);
+        case 7: return launch_dg<D, 7>(stream, p, seqs, nseq);
+        case 8: return launch_dg<D, 8>(stream, p, seqs, nseq);
         default: return hipErrorInvalidValue;
     }
 }
-
-uint32_t rows_per_block(uint32_t g) { return kRowTile * ((g >= 4) ? 1 : (4 + g - 1) / g); }
 
 }  // namespace
 
@@ -581,12 +920,17 @@ bool prefill_supported(const AttnLaunch &a) {
            a.rotary_dim % 32 == 0;
 }
 
+size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows) {
+    return (size_t)total_rows * (a.rotary_dim / 2) * sizeof(float2);
+}
+
 hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
-                               int nseq) {
-    if (nseq <= 0 || nseq > kMetaPerLaunch || !prefill_supported(a)) return hipErrorInvalidValue;
+                               int nseq, void *rope_scratch) {
+    if (nseq <= 0 || nseq > kMetaPerLaunch || !prefill_supported(a) || rope_scratch == nullptr) {
+        return hipErrorInvalidValue;
+    }
     const auto *pool = a.pool;
     const uint32_t g = a.heads / a.kv_heads;
-    const uint32_t rpb = rows_per_block(g);
     PrefillParams p{};
     p.k_pages = pool->k_pages;
     p.v_pages = pool->v_pages;
@@ -598,6 +942,7 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
     p.k_norm = a.k_norm;
     p.positions = a.positions;
     p.out = a.out;
+    p.rope_cs = (float2 *)rope_scratch;
     p.err_word = a.err_word;
     p.num_pages = pool->num_pages;
     p.pages_per_seq = pool->pages_per_seq;
@@ -612,23 +957,10 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
     p.eps = a.eps;
     p.nseq = (uint32_t)nseq;
     p.rope = *a.rope;
-    uint32_t max_blk = 0, max_rows = 0;
-    for (int i = 0; i < nseq; ++i) {
-        PrefillMeta &m = p.meta[i];
-        m.slot = seqs[i].slot;
-        m.ctx = seqs[i].ctx;
-        m.rows = seqs[i].rows;
-        m.row0 = seqs[i].row0;
-        m.nblk = (m.rows + rpb - 1) / rpb;
-        max_blk = std::max(max_blk, m.nblk);
-        max_rows = std::max(max_rows, m.rows);
-    }
-    p.max_blk = max_blk;
-    const uint32_t append_x = (uint32_t)(((uint64_t)max_rows * a.kv_heads + 3) / 4);
     switch (a.head_dim) {
-        case 64: return launch_d<64>(stream, p, g, append_x);
-        case 128: return launch_d<128>(stream, p, g, append_x);
-        case 256: return launch_d<256>(stream, p, g, append_x);
+        case 64: return launch_d<64>(stream, p, g, seqs, nseq);
+        case 128: return launch_d<128>(stream, p, g, seqs, nseq);
+        case 256: return launch_d<256>(stream, p, g, seqs, nseq);
         default: return hipErrorInvalidValue;
     }
 }

@@ -43,19 +43,18 @@ int32_t alloc_page(Pool *pool) {
     return page;
 }
 
-int32_t upload_entries(Ctx *ctx, Pool *pool, uint32_t seq, const std::vector<uint32_t> &index) {
+int32_t upload_entries(Ctx *ctx, Pool *pool, uint32_t seq, const std::vector<uint32_t> &index,
+                       TableBatch *batch) {
     if (index.empty()) {
         return kOk;
     }
-    std::vector<uint32_t> idx(index.size());
-    std::vector<int32_t> val(index.size());
+    TableBatch local;
+    TableBatch &b = batch != nullptr ? *batch : local;
     for (size_t i = 0; i < index.size(); ++i) {
-        idx[i] = seq * pool->pages_per_seq + index[i];
-        val[i] = pool->seqs[seq].pages[index[i]];
+        b.idx.push_back(seq * pool->pages_per_seq + index[i]);
+        b.val.push_back(pool->seqs[seq].pages[index[i]]);
     }
-    SR_HIP(ctx, launch_page_table_set(ctx->stream, pool->d_page_table, idx.data(), val.data(),
-                                      (int)idx.size()));
-    return kOk;
+    return batch != nullptr ? kOk : kv_flush_table(ctx, pool, local);
 }
 
 }  // namespace
@@ -63,7 +62,17 @@ int32_t upload_entries(Ctx *ctx, Pool *pool, uint32_t seq, const std::vector<uin
 // Makes pages [len, len+n) of the sequence writable: copies a shared partial
 // last page, allocates fresh pages, and queues the page-table update.
 // Rejects writes past max_tokens (state.rs:53-55).
-int32_t kv_prepare_append(Ctx *ctx, Pool *pool, uint32_t seq, uint64_t n) {
+int32_t kv_flush_table(Ctx *ctx, Pool *pool, TableBatch &batch) {
+    if (!batch.idx.empty()) {
+        SR_HIP(ctx, launch_page_table_set(ctx->stream, pool->d_page_table, batch.idx.data(),
+                                          batch.val.data(), (int)batch.idx.size()));
+    }
+    batch.idx.clear();
+    batch.val.clear();
+    return kOk;
+}
+
+int32_t kv_prepare_append(Ctx *ctx, Pool *pool, uint32_t seq, uint64_t n, TableBatch *batch) {
     auto &s = pool->seqs[seq];
     const uint64_t new_len = s.len + n;
     if (n == 0 || new_len > pool->max_tokens) {
@@ -97,7 +106,7 @@ int32_t kv_prepare_append(Ctx *ctx, Pool *pool, uint32_t seq, uint64_t n) {
         s.pages.push_back(alloc_page(pool));
         changed.push_back((uint32_t)(s.pages.size() - 1));
     }
-    return upload_entries(ctx, pool, seq, changed);
+    return upload_entries(ctx, pool, seq, changed, batch);
 }
 
 }  // namespace sr

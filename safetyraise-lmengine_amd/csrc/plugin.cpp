@@ -175,7 +175,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_context(
     if (hipStreamSynchronize(context->stream) != hipSuccess) {
         status = kDeviceError;
     }
-    for (DeviceBuffer *b : {&context->staging, &context->partials}) {
+    for (DeviceBuffer *b : {&context->staging, &context->partials, &context->rope_scratch}) {
         if (b->ptr != nullptr) (void)hipFree(b->ptr);
     }
     if (context->d_error_word != nullptr) (void)hipFree(context->d_error_word);

@@ -68,6 +68,7 @@ struct safetyraise_kernel_context {
     uint32_t *d_error_word = nullptr;  // sticky kernel-detected errors
     sr::DeviceBuffer staging;          // host-pointer mode device copies
     sr::DeviceBuffer partials;         // split-K partial (m, l, o) records
+    sr::DeviceBuffer rope_scratch;     // prefill: per-row RoPE cos/sin
     float rope_theta = 0.0f;
     uint32_t rope_dim = 0;
     sr::RopeTable rope{};
@@ -143,8 +144,16 @@ int32_t take_error_word(Ctx *ctx, uint32_t *word);
 int32_t error_word_status(Ctx *ctx, uint32_t word);
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim);
 
-// KV pool helpers used by attention.
-int32_t kv_prepare_append(Ctx *ctx, safetyraise_kernel_kv_pool *pool, uint32_t seq, uint64_t n);
+// KV pool helpers used by attention.  Page-table entries changed by
+// kv_prepare_append are queued in `batch` when it is given (and uploaded by
+// kv_flush_table in one launch), else uploaded at once.
+struct TableBatch {
+    std::vector<uint32_t> idx;
+    std::vector<int32_t> val;
+};
+int32_t kv_prepare_append(Ctx *ctx, safetyraise_kernel_kv_pool *pool, uint32_t seq, uint64_t n,
+                          TableBatch *batch = nullptr);
+int32_t kv_flush_table(Ctx *ctx, safetyraise_kernel_kv_pool *pool, TableBatch &batch);
 
 // ---------------- kernel launchers (defined in the .hip files) ----------------
 hipError_t launch_page_table_set(hipStream_t s, int32_t *table, const uint32_t *idx,
@@ -190,8 +199,12 @@ hipError_t launch_attn_decode(hipStream_t s, const AttnLaunch &a, const SeqMeta 
 // Chunked prefill: seqs[i].rows new rows appended after seqs[i].ctx cached
 // tokens, row i attending to ctx + i + 1 keys.  Up to kMetaPerLaunch
 // sequences; only for geometries where prefill_supported() holds.
+// rope_scratch holds prefill_rope_bytes(a, rows of the call) bytes (per-row
+// RoPE cos/sin shared by the two kernels).
 bool prefill_supported(const AttnLaunch &a);
-hipError_t launch_attn_prefill(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq);
+size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows);
+hipError_t launch_attn_prefill(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
+                               void *rope_scratch);
 
 struct GdnLaunch {
     const safetyraise_kernel_gdn_pool *pool;
