@@ -42,7 +42,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="decode", choices=["decode", "prefill", "copy"])
+    p.add_argument("--workload", default="decode",
+                   choices=["decode", "prefill", "gdn-decode", "gdn-prefill", "copy"])
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
     p.add_argument("--prefill-steps", type=int, default=5)
@@ -411,6 +412,271 @@ def cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim, chunk):
     }
 
 
+VALU_F32_PEAK_TFS = 157.3  # MI355X vector fp32
+
+
+def gdn_layer_setup(torch, pkg, backend, gen, hk, hv, dk, dv, K, nseq):
+    """Seeded GDN layer (BASELINE config 4 draws: A_log 0, dt_bias 0, conv ~N(0,1)/2,
+    norm 1) and a state pool whose sequences start from a N(0, 0.02) state."""
+    C_ = 2 * hk * dk + hv * dv
+    layer = {
+        "a_log": torch.zeros(hv, device="cuda"),
+        "dt_bias": torch.zeros(hv, device="cuda"),
+        "conv": (torch.randn((C_, K), generator=gen, device="cuda") / 2),
+        "norm": torch.ones(dv, device="cuda"),
+    }
+    pool = pkg.GdnState(backend, hk, hv, dk, dv, K, nseq)
+    ids = [pool.open() for _ in range(nseq)]
+    return layer, pool, ids, C_
+
+
+def gdn_args(pkg, pool, ids_c, rows_c, nseq, x, layer, out, asynchronous=True):
+    P = pkg.plugin
+    a = P.GdnArgs()
+    a.struct_size = C.sizeof(P.GdnArgs)
+    a.flags = P.DEVICE_POINTERS | (P.ASYNC if asynchronous else 0)
+    a.eps = 1e-6
+    a.num_seqs = nseq
+    a.seq_ids, a.seq_rows = ids_c, rows_c
+    qkv, z, av, bv = x
+    a.qkv, a.z, a.a, a.b = qkv.data_ptr(), z.data_ptr(), av.data_ptr(), bv.data_ptr()
+    a.a_log, a.dt_bias = layer["a_log"].data_ptr(), layer["dt_bias"].data_ptr()
+    a.conv_weight, a.norm = layer["conv"].data_ptr(), layer["norm"].data_ptr()
+    a.out = out.data_ptr()
+    a.state = pool.handle
+    return a
+
+
+def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
+    """BASELINE config 4, decode: Qwen3.5-style GDN, Hk 16 / Hv 32, d 128, conv 4,
+    batch 8, one token per sequence; one step = one token through `layers`
+    independent GDN layers.  HBM-bound: algorithmic bytes = state read + write,
+    conv history read + write, the inputs, the conv weights and the output."""
+    hk, hv, dk, dv, K, nseq = 16, 32, 128, 128, 4, 8
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0003)
+    rng = np.random.default_rng(0x5A5A0003)
+    P = pkg.plugin
+    pools, all_args, layer_w = [], [], []
+    total = warmup + steps
+    outs = torch.empty((layers, nseq, hv * dv), device="cuda")
+    for l in range(layers):
+        layer, pool, ids, C_ = gdn_layer_setup(torch, pkg, backend, gen, hk, hv, dk, dv, K, nseq)
+        for s in ids:
+            m = (0.02 * rng.standard_normal((hv, dv, dk))).astype(np.float32)
+            hst = (0.5 * rng.standard_normal((C_, K - 1))).astype(np.float32)
+            pool.write(s, m, hst)
+        xs = [(torch.randn((nseq, C_), generator=gen, device="cuda"),
+               torch.randn((nseq, hv * dv), generator=gen, device="cuda"),
+               torch.randn((nseq, hv), generator=gen, device="cuda"),
+               torch.randn((nseq, hv), generator=gen, device="cuda")) for _ in range(2)]
+        ids_c = (C.c_uint32 * nseq)(*ids)
+        rows_c = (C.c_uint32 * nseq)(*([1] * nseq))
+        all_args.append([gdn_args(pkg, pool, ids_c, rows_c, nseq, xs[i], layer, outs[l])
+                         for i in range(2)])
+        pools.append((pool, ids_c, rows_c, xs))
+        layer_w.append(layer)
+    backend.synchronize()
+    fwd = backend.lib.safetyraise_kernel_gdn_forward
+    ctx = backend.context
+
+    def run(step, events=None):
+        for l in range(layers):
+            if events is not None:
+                events[l][0].record(stream)
+            st = fwd(ctx, C.byref(all_args[l][step & 1]))
+            if events is not None:
+                events[l][1].record(stream)
+            if st != 0:
+                backend.check(st, "gdn_forward")
+
+    for s in range(warmup):
+        run(s)
+    backend.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(layers)] for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for s in range(steps):
+        run(warmup + s, ev[s])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    C_ = 2 * hk * dk + hv * dv
+    per_layer = (2 * nseq * hv * dv * dk * 4          # state read + write
+                 + 2 * nseq * C_ * (K - 1) * 4        # conv history read + write
+                 + nseq * (C_ + hv * dv + 2 * hv) * 4  # qkv, z, a, b
+                 + C_ * K * 4                         # conv weights
+                 + nseq * hv * dv * 4)                # output
+    ms = t0.elapsed_time(t1) / steps
+    call_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev])
+    value = per_layer * layers / (ms * 1e-3) / 1e9
+    achieved = per_layer / (call_us.mean() * 1e-6) / 1e9
+    result = {
+        "workload": f"qwen3.5 GDN decode (BASELINE config 4): Hk 16 / Hv 32, d 128, conv 4, "
+                    f"batch 8, {layers} layers per step",
+        "value": round(value, 2), "unit": "GB/s",
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "dtype": "f32",
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("gdn_decode_qwen35"),
+            "kernel": "gdn_delta_kernel + gdn_norm_gate_kernel",
+            "launch_us_mean": round(float(call_us.mean()), 2),
+            "bytes_per_launch": int(per_layer),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_gdn(pools[0][0], pools[0][1], pools[0][3][0],
+                                                  layer_w[0], hk, hv, dk, dv, K, nseq, 1,
+                                                  per_layer, "GB/s")
+    for pool, *_ in pools:
+        pool.destroy()
+    backend.close()
+    return result
+
+
+def bench_gdn_prefill(args, torch, pkg, steps, warmup):
+    """BASELINE config 4, prefill: 2 sequences x 2048 tokens in chunks of 64 (32 calls
+    per layer); one step = the whole prefill of one layer from a zero state.  The
+    kernel runs the recurrence token by token with the state held in registers
+    (VALU f32); FLOPs count 7 * Dk * Dv per (row, value head), the token-serial
+    work (decay, predict, correct, read)."""
+    hk, hv, dk, dv, K, nseq, total, chunk = 16, 32, 128, 128, 4, 2, 2048, 64
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0004)
+    layer, pool, ids, C_ = gdn_layer_setup(torch, pkg, backend, gen, hk, hv, dk, dv, K, nseq)
+    nchunk = total // chunk
+    rows = nseq * chunk
+    xs = [(torch.randn((rows, C_), generator=gen, device="cuda"),
+           torch.randn((rows, hv * dv), generator=gen, device="cuda"),
+           torch.randn((rows, hv), generator=gen, device="cuda"),
+           torch.randn((rows, hv), generator=gen, device="cuda")) for _ in range(nchunk)]
+    out = torch.empty((rows, hv * dv), device="cuda")
+    zero_m = np.zeros((hv, dv, dk), np.float32)
+    zero_h = np.zeros((C_, K - 1), np.float32)
+    fwd = backend.lib.safetyraise_kernel_gdn_forward
+    ctx = backend.context
+
+    def make(ids_now):
+        ids_c = (C.c_uint32 * nseq)(*ids_now)
+        rows_c = (C.c_uint32 * nseq)(*([chunk] * nseq))
+        return [gdn_args(pkg, pool, ids_c, rows_c, nseq, xs[c], layer, out) for c in range(nchunk)]
+
+    state = {"ids": ids, "args": make(ids)}
+
+    def reset():
+        # a fresh prompt: new sequences start from a zero state and history
+        for s in state["ids"]:
+            pool.close(s)
+        state["ids"] = [pool.open() for _ in range(nseq)]
+        state["args"] = make(state["ids"])
+
+    def run(events=None):
+        for c in range(nchunk):
+            if events is not None:
+                events[c][0].record(stream)
+            st = fwd(ctx, C.byref(state["args"][c]))
+            if events is not None:
+                events[c][1].record(stream)
+            if st != 0:
+                backend.check(st, "gdn_forward")
+
+    for _ in range(warmup):
+        reset()
+        run()
+    backend.synchronize()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(nchunk)] for _ in range(steps)]
+    total_ms = 0.0
+    for s in range(steps):
+        reset()  # host bookkeeping and a state clear, outside the timed region
+        backend.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        run(ev[s])
+        t1.record(stream)
+        torch.cuda.synchronize()
+        total_ms += t0.elapsed_time(t1)
+    backend.synchronize()
+    ms = total_ms / steps
+    flops = 7 * dk * dv * hv * nseq * total
+    tflops = flops / (ms * 1e-3) / 1e12
+    call_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev])
+    call_tf = flops / (call_us.sum(1).mean() * 1e-6) / 1e12
+    chunked_form = 28.3e9  # flops of the chunked (WY) form for the same work
+    result = {
+        "workload": "qwen3.5 GDN prefill (BASELINE config 4): 2 x 2048 tokens in chunks of 64, "
+                    "one layer per step, from a zero state",
+        "value": round(tflops, 3), "unit": "TFLOP/s",
+        "pct_of_valu_f32_peak": round(100 * tflops / VALU_F32_PEAK_TFS, 2),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "gflop_per_step_token_serial": round(flops / 1e9, 2),
+        "chunked_form_equivalent_tflops": round(chunked_form / (ms * 1e-3) / 1e12, 3),
+        "dtype": "f32 (VALU, token-serial recurrence)",
+        "roofline": {
+            "bound": "valu-f32", "achieved": round(call_tf, 3), "peak": VALU_F32_PEAK_TFS,
+            "unit": "TFLOP/s", "frac": round(call_tf / VALU_F32_PEAK_TFS, 4),
+            "traffic": traffic_from_profiles("gdn_prefill_qwen35"),
+            "kernel": "gdn_delta_kernel + gdn_norm_gate_kernel",
+            "launch_us_mean": round(float(call_us.mean()), 2),
+            "flops_per_step": int(flops),
+        },
+    }
+    if not args.no_cpu:
+        ids_c = (C.c_uint32 * nseq)(*state["ids"])
+        result["cpu_baseline"] = cpu_baseline_gdn(pool, ids_c, xs[0][0], layer, hk, hv, dk, dv,
+                                                  K, 1, chunk, 7 * dk * dv * hv * chunk,
+                                                  "GFLOP/s")
+    pool.destroy()
+    backend.close()
+    return result
+
+
+def cpu_baseline_gdn(pool, ids_c, qkv_dev, layer, hk, hv, dk, dv, K, nseq, rows, work, unit):
+    """CPU oracle (1 thread: the reference's row loop is serial) on `nseq` sequences x
+    `rows` rows of the same layer shape, from the GPU pool's current state."""
+    from oracle import pyoracle as O
+
+    rng = np.random.default_rng(7)
+    C_ = 2 * hk * dk + hv * dv
+    conv = layer["conv"].cpu().numpy()
+    a_log = layer["a_log"].cpu().numpy()
+    dt_bias = layer["dt_bias"].cpu().numpy()
+    norm = layer["norm"].cpu().numpy()
+    t = 0.0
+    for i in range(nseq):
+        m, hst = pool.read(ids_c[i])
+        qkv = rng.standard_normal((rows, C_)).astype(np.float32)
+        z = rng.standard_normal((rows, hv * dv)).astype(np.float32)
+        a = rng.standard_normal((rows, hv)).astype(np.float32)
+        b = rng.standard_normal((rows, hv)).astype(np.float32)
+        t0 = time.perf_counter()
+        O.gdn_rows(qkv, z, a, b, a_log, dt_bias, conv, K, norm, 1e-6, key_heads=hk,
+                   value_heads=hv, key_dim=dk, value_dim=dv, history=hst, state=m)
+        t += time.perf_counter() - t0
+    scale = 1e9 if unit in ("GB/s", "GFLOP/s") else 1.0
+    per_item = work / nseq if unit == "GB/s" else work
+    return {"value": round(per_item * nseq / t / scale, 3), "unit": unit, "cores": 1,
+            "kind": "port",
+            "sample": f"{nseq} sequence(s) x {rows} row(s) of the same layer shape, f32 oracle",
+            "ms": round(t * 1e3, 2)}
+
+
 def bench_copy(args, torch):
     """Calibration: a plain device copy of a known size (for PMC byte counters)."""
     nbytes = 1 << 30
@@ -449,6 +715,14 @@ def main():
         result = bench_decode(args, torch, pkg)
         if not args.no_prefill:
             result["prefill"] = bench_prefill(args, torch, pkg, args.prefill_steps, 2)
+            result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 10, 3)
+            result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 3, 1)
+    elif args.workload in ("gdn-decode", "gdn-prefill"):
+        fn = bench_gdn_decode if args.workload == "gdn-decode" else bench_gdn_prefill
+        result = fn(args, torch, pkg, args.steps, args.warmup)
+        result = {"metric": "GDN " + args.workload[4:] + " " + result["unit"], "n_gpus": 1,
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "data": "synthetic", "config": {"workload": result.pop("workload")}, **result}
     elif args.workload == "prefill":
         result = bench_prefill(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "prefill attn TFLOP/s, Qwen3-8B GQA shape", "n_gpus": 1,
