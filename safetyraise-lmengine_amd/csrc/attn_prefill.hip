@@ -419,15 +419,20 @@ __device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase,
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
+    // (one branch around all loads of a format, so that they are in flight
+    // together)
     float x[NS][8];
+    if (bf16_in) {
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
-        const size_t off = qbase + 16 * st + 8 * h;
-        if (bf16_in) {
-            const u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + off);
+        for (int st = 0; st < NS; ++st) {
+            const u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + qbase + 16 * st + 8 * h);
 #pragma unroll
             for (int j = 0; j < 8; ++j) x[st][j] = bf16_elem(w, j);
-        } else {
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const size_t off = qbase + 16 * st + 8 * h;
             const float4 a = *(const float4 *)((const float *)p.q + off);
             const float4 c = *(const float4 *)((const float *)p.q + off + 4);
             x[st][0] = a.x; x[st][1] = a.y; x[st][2] = a.z; x[st][3] = a.w;

@@ -43,6 +43,16 @@ __device__ __forceinline__ float load_act(const void *p, size_t i, bool bf16) {
     return bf16 ? bf16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i];
 }
 
+// The same without a branch: one 32-bit load of the aligned word that holds
+// element i (the element itself for f32), then a select.  Loads behind a
+// branch end in a wait for every load in flight; these stay in flight.
+__device__ __forceinline__ float load_act_nb(const void *p, size_t i, bool bf16) {
+    const uint32_t *w = (const uint32_t *)p + (bf16 ? (i >> 1) : i);
+    const uint32_t x = *w;
+    const uint32_t bits = bf16 ? ((i & 1) ? (x & 0xffff0000u) : (x << 16)) : x;
+    return __uint_as_float(bits);
+}
+
 // DPP controls (gfx9 encoding): quad permutes, half-row and row mirrors.
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
