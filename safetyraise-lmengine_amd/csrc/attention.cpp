@@ -55,6 +55,19 @@ int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta
     return kOk;
 }
 
+int32_t run_verify_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
+    DecodePlanInput plan{ctx->num_cus, reserve_partials, ctx};
+    const hipError_t e = launch_attn_verify(ctx->stream, a, pack.data(), (int)pack.size(),
+                                            ctx->rope_scratch.ptr, plan);
+    if (e != hipSuccess) {
+        if (ctx->error.empty() || e != hipErrorOutOfMemory) {
+            return hip_fail(ctx, e, "verify attention launch");
+        }
+        return kNoMemory;
+    }
+    return kOk;
+}
+
 int32_t run_prefill_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
     const hipError_t e =
         launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size(), ctx->rope_scratch.ptr);
@@ -215,9 +228,35 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         int32_t st = ensure_buffer(ctx, ctx->rope_scratch, prefill_rope_bytes(L, total_rows), false);
         if (st != kOk) return st;
     }
+    // Sequences with 2..15 rows (MTP verify drafts) take the multi-row
+    // split-K kernel: every cached K/V tile is read once for all rows.
     {
         std::vector<SeqMeta> pack;
         for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            if (A.seq_rows[i] >= kPrefillMinRows || !verify_supported(L, A.seq_rows[i])) continue;
+            serial[i] = 0;
+            any_prefill = true;
+            SeqMeta m{};
+            m.slot = A.seq_ids[i];
+            m.ctx = (uint32_t)old_len[i];
+            m.rows = A.seq_rows[i];
+            m.row0 = (uint32_t)row0[i];
+            pack.push_back(m);
+            if (pack.size() == (size_t)kMetaPerLaunch) {
+                int32_t st = run_verify_pack(ctx, L, pack);
+                if (st != kOk) return st;
+                pack.clear();
+            }
+        }
+        if (!pack.empty()) {
+            int32_t st = run_verify_pack(ctx, L, pack);
+            if (st != kOk) return st;
+        }
+    }
+    {
+        std::vector<SeqMeta> pack;
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            if (!serial[i]) continue;
             if (!prefill_ok || A.seq_rows[i] < kPrefillMinRows) {
                 serial_rows = std::max(serial_rows, A.seq_rows[i]);
                 continue;

@@ -917,25 +917,213 @@ hipError_t launch_d(hipStream_t stream, PrefillParams &p, uint32_t g, const SeqM
     }
 }
 
-}  // namespace
 
-bool prefill_supported(const AttnLaunch &a) {
-    const uint32_t g = a.heads / a.kv_heads;
-    return (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) && g >= 1 && g <= 8 &&
-           a.rotary_dim % 32 == 0;
-}
+// ---------------------------------------------------------------------------
+// Multi-row verify (MTP drafts): split-K flash decoding with MFMA inner
+// products.  A call appends R (2..15) rows per sequence; row r sees the
+// context plus rows 0..r.  The R x G query vectors of a KV head (row r, head
+// g: vector r*G + g) fill the N dimension of the MFMA tiles, 32 per wave, so
+// each K/V tile of the cache is read once for all rows and heads.  The keys
+// of a sequence are cut into partitions of part_keys (a multiple of 64); one
+// workgroup per (partition, KV head) runs the online softmax over its keys
+// and leaves a (max, sum, o[D]) record per query vector, which
+// attn_verify_combine_kernel merges (math.rs:133-152 split over the keys).
+// ---------------------------------------------------------------------------
+struct VerifyParams {
+    PrefillParams p;       // meta[s].nblk = partitions of sequence s
+    float *partials;       // records of kRecordStride floats
+    uint32_t part_keys;
+    uint32_t rows_g;       // query vectors per KV head of the widest sequence (<= 64)
+    uint32_t blk0[kMetaPerLaunch];  // first partition of each sequence (prefix)
+    uint32_t rec0[kMetaPerLaunch];  // first record of each sequence
+};
 
-size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows) {
-    return (size_t)total_rows * (a.rotary_dim / 2) * sizeof(float2);
-}
+template <int D>
+constexpr int kRecordStride = D + 4;  // m, l, 2 unused, o[D] (16-byte aligned)
 
-hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
-                               int nseq, void *rope_scratch) {
-    if (nseq <= 0 || nseq > kMetaPerLaunch || !prefill_supported(a) || rope_scratch == nullptr) {
-        return hipErrorInvalidValue;
+// Four waves stage every tile; the waves that hold query vectors (32 each,
+// at most two) also run the products.
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_verify_kernel(
+    const VerifyParams vp) {
+    constexpr int NS = D / 16;
+    constexpr int NT = D / 32;
+    using Io = TileIo<D, 256, false>;
+    extern __shared__ __align__(16) unsigned char lds[];
+    const PrefillParams &p = vp.p;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const uint32_t kvh = blockIdx.x % p.kv_heads;
+    const uint32_t j = blockIdx.x / p.kv_heads;
+    uint32_t s = 0;
+    while (s + 1 < p.nseq && vp.blk0[s + 1] <= j) ++s;
+    const PrefillMeta m = p.meta[s];
+    const uint32_t part = j - vp.blk0[s];
+    const uint32_t G = p.heads / p.kv_heads;
+    const uint32_t nvec = m.rows * G;
+    const bool computes = 32u * wave < nvec;               // wave-uniform
+    const uint32_t vec = min(32u * wave + col, nvec - 1);  // this lane's query vector
+    const uint32_t r = vec / G;
+    const uint32_t head = kvh * G + vec % G;
+    const uint32_t total = m.ctx + m.rows;
+    const uint32_t key_begin = part * vp.part_keys;
+    const uint32_t key_end = min(key_begin + vp.part_keys, total);
+    const uint32_t key_limit = m.ctx + r;
+
+    BlockPos b;
+    b.m = m;
+    b.kvh = kvh;
+    b.row0 = 0;
+    b.n_keys = total;
+    b.n_tiles = (total + kKeyTile - 1) / kKeyTile;
+    b.active = true;
+    Io io;
+    io.init(tid, p, b);
+    u32x4 kreg[Io::KL];
+    u32x4 vreg[4 * Io::VL];
+    const uint32_t t0 = key_begin / kKeyTile;
+    const uint32_t t1 = (key_end + kKeyTile - 1) / kKeyTile;
+    io.load_k(kreg, t0, 0);
+    io.load_v(vreg, t0, 0);
+    const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
+    const size_t qbase = (size_t)(m.row0 + r) * p.heads * hs + (size_t)head * hs;
+    f16x8 qop[NS];
+    if (computes) q_operands<D>(p, qbase, m.row0 + r, h, lane, qop);
+
+    f32x16 oacc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    for (uint32_t t = t0; t < t1; ++t) {
+        unsigned char *kt = lds + (t & 1) * 2 * kTileBytes<D>;
+        unsigned char *vt = kt + kTileBytes<D>;
+        const uint32_t key0 = t * kKeyTile;
+        io.store_k(kreg, kt);
+        io.store_v(vreg, vt, min(key_end, total) - key0);
+        __syncthreads();
+        if (t + 1 < t1) {
+            io.load_k(kreg, t + 1, 0);
+            io.load_v(vreg, t + 1, 0);
+        }
+        if (computes) {
+            f32x16 sacc[2];
+            s_tile<D>(kt, qop, h, col, sacc);
+            // keys past the partition end (the last tile of the sequence)
+            // and past a row's own position are masked
+            const bool edge = key0 + kKeyTile > min(key_end, m.ctx + 1);
+            if (edge) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+                        if (key >= key_end) sacc[u][i] = -INFINITY;
+                    }
+            }
+            f16x8 pop[4];
+            softmax_tile<D>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
+            pv_tile<D>(vt, pop, h, col, oacc);
+        }
     }
+    const float l = xhalf_sum(l_run);
+    if (32u * wave + col >= nvec) return;
+    // record of (sequence s, row r, head g, partition): o unnormalised
+    const uint32_t nparts = m.nblk;
+    float *rec = vp.partials +
+                 ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nparts + part) *
+                     kRecordStride<D>;
+    if (h == 0) {
+        // a partition whose keys are all past this row's limit has l = 0
+        *(float2 *)rec = make_float2(l > 0.0f ? m_run : -INFINITY, l);
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const uint32_t d0 = 32 * tt + 8 * a + 4 * h;
+            *(float4 *)(rec + 4 + d0) = make_float4(oacc[tt][4 * a], oacc[tt][4 * a + 1],
+                                                    oacc[tt][4 * a + 2], oacc[tt][4 * a + 3]);
+        }
+}
+
+// One wave per (sequence, row, head): merges the partition records in the
+// log2 domain, divides by the sum, applies the Qwen3.5 gate and stores.
+template <int D>
+__global__ __launch_bounds__(256) void attn_verify_combine_kernel(const VerifyParams vp) {
+    constexpr int EPL = D / 64;
+    const PrefillParams &p = vp.p;
+    const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    uint32_t s = 0, base = 0;
+    for (; s < p.nseq; ++s) {
+        const uint32_t n = p.meta[s].rows * p.heads;
+        if (w < base + n) break;
+        base += n;
+    }
+    if (s >= p.nseq) return;
+    const PrefillMeta m = p.meta[s];
+    const uint32_t r = (w - base) / p.heads;
+    const uint32_t head = (w - base) % p.heads;
+    const uint32_t nparts = m.nblk;
+    const float *rec = vp.partials +
+                       ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nparts) * kRecordStride<D>;
+    float mx = -INFINITY;
+    for (uint32_t q = 0; q < nparts; ++q) mx = fmaxf(mx, rec[(size_t)q * kRecordStride<D>]);
+    float l = 0.0f;
+    float o[EPL] = {};
+    for (uint32_t q = 0; q < nparts; ++q) {
+        const float *rq = rec + (size_t)q * kRecordStride<D>;
+        const float mq = rq[0];
+        if (mq == -INFINITY) continue;  // no visible key in this partition
+        const float sc = fast_exp2(mq - mx);
+        l += rq[1] * sc;
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) o[i] += rq[4 + lane + 64 * i] * sc;
+    }
+    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
+    const uint32_t hs = gated ? 2 * D : D;
+    const size_t qbase = (size_t)(m.row0 + r) * p.heads * hs + (size_t)head * hs;
+    float *dst = p.out + (size_t)(m.row0 + r) * p.heads * D + (size_t)head * D;
+    const float inv = 1.0f / l;
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        float y = o[i] * inv;
+        finite = finite && isfinite(y);
+        if (gated) y *= ref_sigmoid(load_act(p.q, qbase + D + lane + 64 * i, bf16_in));
+        dst[lane + 64 * i] = y;
+    }
+    if (!finite) atomicOr(p.err_word, kErrPrefillRange);
+}
+
+template <int D>
+hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
+                           uint32_t combine_waves) {
+    static bool configured = false;
+    const size_t lds = 4 * kTileBytes<D>;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute((const void *)attn_verify_kernel<D>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(attn_verify_kernel<D>, dim3(blocks), dim3(256), lds, stream, vp);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_verify_combine_kernel<D>, dim3((combine_waves + 3) / 4), dim3(256), 0,
+                       stream, vp);
+    return hipGetLastError();
+}
+
+PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
     const auto *pool = a.pool;
-    const uint32_t g = a.heads / a.kv_heads;
     PrefillParams p{};
     p.k_pages = pool->k_pages;
     p.v_pages = pool->v_pages;
@@ -962,12 +1150,89 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
     p.eps = a.eps;
     p.nseq = (uint32_t)nseq;
     p.rope = *a.rope;
+    return p;
+}
+
+}  // namespace
+
+bool prefill_supported(const AttnLaunch &a) {
+    const uint32_t g = a.heads / a.kv_heads;
+    return (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) && g >= 1 && g <= 8 &&
+           a.rotary_dim % 32 == 0;
+}
+
+size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows) {
+    return (size_t)total_rows * (a.rotary_dim / 2) * sizeof(float2);
+}
+
+hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
+                               int nseq, void *rope_scratch) {
+    if (nseq <= 0 || nseq > kMetaPerLaunch || !prefill_supported(a) || rope_scratch == nullptr) {
+        return hipErrorInvalidValue;
+    }
+    const uint32_t g = a.heads / a.kv_heads;
+    PrefillParams p = fill_params(a, nseq, rope_scratch);
     switch (a.head_dim) {
         case 64: return launch_d<64>(stream, p, g, seqs, nseq);
         case 128: return launch_d<128>(stream, p, g, seqs, nseq);
         case 256: return launch_d<256>(stream, p, g, seqs, nseq);
         default: return hipErrorInvalidValue;
     }
+}
+
+bool verify_supported(const AttnLaunch &a, uint32_t rows) {
+    return prefill_supported(a) && a.head_dim <= 128 && rows >= 2 &&
+           rows * (a.heads / a.kv_heads) <= 64;
+}
+
+hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
+                              int nseq, void *rope_scratch, const DecodePlanInput &in) {
+    if (nseq <= 0 || nseq > kMetaPerLaunch || rope_scratch == nullptr) return hipErrorInvalidValue;
+    const uint32_t g = a.heads / a.kv_heads;
+    VerifyParams vp{};
+    vp.p = fill_params(a, nseq, rope_scratch);
+    PrefillParams &p = vp.p;
+    // partition size: about 2 workgroups per CU over the whole call, at
+    // least 256 keys, a multiple of the 64-key tile
+    uint64_t keys = 0;
+    uint32_t max_rows = 0, rows_g = 0;
+    for (int i = 0; i < nseq; ++i) {
+        if (!verify_supported(a, seqs[i].rows)) return hipErrorInvalidValue;
+        keys += (uint64_t)seqs[i].ctx + seqs[i].rows;
+        max_rows = std::max(max_rows, seqs[i].rows);
+        rows_g = std::max(rows_g, seqs[i].rows * g);
+    }
+    const uint64_t target = (uint64_t)std::max(in.num_cus, 1) * 2;
+    uint64_t part = (keys * a.kv_heads + target - 1) / target;
+    part = std::max<uint64_t>(256, (part + kKeyTile - 1) / kKeyTile * kKeyTile);
+    vp.part_keys = (uint32_t)std::min<uint64_t>(part, 1u << 30);
+    vp.rows_g = rows_g;
+    uint32_t blocks = 0, records = 0, waves = 0;
+    for (int i = 0; i < nseq; ++i) {
+        PrefillMeta &m = p.meta[i];
+        m.slot = seqs[i].slot;
+        m.ctx = seqs[i].ctx;
+        m.rows = seqs[i].rows;
+        m.row0 = seqs[i].row0;
+        m.nblk = (m.ctx + m.rows + vp.part_keys - 1) / vp.part_keys;
+        vp.blk0[i] = blocks;
+        vp.rec0[i] = records;
+        blocks += m.nblk;
+        records += m.nblk * m.rows * a.heads;
+        waves += m.rows * a.heads;
+    }
+    p.max_blk = 0;
+    const size_t stride = (a.head_dim == 64 ? kRecordStride<64> : kRecordStride<128>);
+    vp.partials = in.reserve_partials((size_t)records * stride * sizeof(float));
+    if (vp.partials == nullptr) return hipErrorOutOfMemory;
+    // K/V of the new rows and their RoPE cos/sin first (append kernel)
+    hipLaunchKernelGGL(a.head_dim == 64 ? kv_append_rows_kernel<64> : kv_append_rows_kernel<128>,
+                       dim3(max_rows, p.nseq), dim3(256), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t grid = blocks * a.kv_heads;
+    if (a.head_dim == 64) return launch_verify_d<64>(stream, vp, grid, waves);
+    return launch_verify_d<128>(stream, vp, grid, waves);
 }
 
 }  // namespace sr

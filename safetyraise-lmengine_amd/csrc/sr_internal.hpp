@@ -205,6 +205,12 @@ bool prefill_supported(const AttnLaunch &a);
 size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows);
 hipError_t launch_attn_prefill(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
                                void *rope_scratch);
+// Multi-row verify (2..15 rows per sequence, rows x heads/kv_heads <= 64,
+// head_dim <= 128): split-K over key partitions with MFMA inner products,
+// then a combine pass; partial records come from in.reserve_partials.
+bool verify_supported(const AttnLaunch &a, uint32_t rows);
+hipError_t launch_attn_verify(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
+                              void *rope_scratch, const DecodePlanInput &in);
 
 struct GdnLaunch {
     const safetyraise_kernel_gdn_pool *pool;
