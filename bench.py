@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "prefill", "gdn-decode", "gdn-prefill", "copy"])
+                   choices=["decode", "prefill", "verify", "gdn-decode", "gdn-prefill", "copy"])
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
     p.add_argument("--prefill-steps", type=int, default=5)
@@ -677,6 +677,150 @@ def cpu_baseline_gdn(pool, ids_c, qkv_dev, layer, hk, hv, dk, dv, K, nseq, rows,
             "ms": round(t * 1e3, 2)}
 
 
+def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
+    """long-context MTP speculative-verify attention, Qwen3-32B
+    shape: 64 Q / 8 KV heads, head_dim 128, 1 + 4 draft rows per sequence (row j
+    sees 131072 + j + 1 keys), batch 4, context 131072, paged bf16 KV in 16-token
+    pages whose order interleaves the four sequences at random.  One step = one
+    verify call; the drafts are truncated away afterwards (the next step verifies
+    at the same context).  Inputs ~N(0,1) are taken as normalised (no QK-norm);
+    RoPE is applied as part of the fused path."""
+    heads, kvh, dim, nseq, ctx_len, page = 64, 8, 128, 4, 131072, 16
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0005)
+    rng = np.random.default_rng(0x5A5A0005)
+    max_tokens = ctx_len + rows + 16
+    pool = pkg.KvCache(backend, kvh, dim, page, nseq * (max_tokens // page + 2) + 8, max_tokens,
+                       nseq)
+    ids = [pool.open() for _ in range(nseq)]
+    # fill in random-length runs of whole pages, sequences in random order,
+    # so each sequence's pages are spread over the pool
+    kfull = torch.randn((ctx_len, kvh * dim), generator=gen, device="cuda", dtype=torch.bfloat16)
+    vfull = torch.randn((ctx_len, kvh * dim), generator=gen, device="cuda", dtype=torch.bfloat16)
+    filled = [0] * nseq
+    while min(filled) < ctx_len:
+        order = [i for i in range(nseq) if filled[i] < ctx_len]
+        rng.shuffle(order)
+        for i in order:
+            n = min(page * int(rng.integers(1, 9)) if interleave else ctx_len, ctx_len - filled[i])
+            pool.append(ids[i], kfull[filled[i]:filled[i] + n], vfull[filled[i]:filled[i] + n],
+                        flags=pkg.ASYNC)
+            filled[i] += n
+    backend.synchronize()
+    del kfull, vfull
+    q = torch.randn((nseq * rows, heads * dim), generator=gen, device="cuda")
+    k = torch.randn((nseq * rows, kvh * dim), generator=gen, device="cuda")
+    v = torch.randn((nseq * rows, kvh * dim), generator=gen, device="cuda")
+    out = torch.empty((nseq * rows, heads * dim), device="cuda")
+    pos = torch.tensor([[ctx_len + r] * 3 for _ in range(nseq) for r in range(rows)],
+                       dtype=torch.int32, device="cuda")
+    P = pkg.plugin
+    a = P.AttentionArgs()
+    a.struct_size = C.sizeof(P.AttentionArgs)
+    a.flags = P.DEVICE_POINTERS | P.ASYNC | P.MROPE_INTERLEAVED
+    a.heads, a.kv_heads, a.head_dim, a.rotary_dim = heads, kvh, dim, dim
+    a.eps, a.rope_theta = 1e-6, 1e6
+    a.num_seqs = nseq
+    a.seq_ids = (C.c_uint32 * nseq)(*ids)
+    a.seq_rows = (C.c_uint32 * nseq)(*([rows] * nseq))
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.positions = pos.data_ptr()
+    a.out = out.data_ptr()
+    a.kv = pool.handle
+    fwd = backend.lib.safetyraise_kernel_attention_forward
+    ctx = backend.context
+
+    def run(events=None):
+        if events is not None:
+            events[0].record(stream)
+        st = fwd(ctx, C.byref(a))
+        if events is not None:
+            events[1].record(stream)
+        if st != 0:
+            backend.check(st, "attention_forward")
+        for s_ in ids:
+            pool.truncate(s_, ctx_len)  # host bookkeeping only
+
+    for _ in range(warmup):
+        run()
+    backend.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for s_ in range(steps):
+        run(ev[s_])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    call_us = np.array([x.elapsed_time(y) * 1e3 for x, y in ev])
+    keys = sum(ctx_len + j + 1 for j in range(rows))  # per sequence, summed over rows
+    nbytes = nseq * (ctx_len + rows) * kvh * dim * 2 * 2
+    flops = nseq * heads * 4 * dim * keys
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    achieved = nbytes / (call_us.mean() * 1e-6) / 1e9
+    result = {
+        "workload": "qwen3-32b MTP verify attention (BASELINE config 5): 64 Q / 8 KV heads, "
+                    "d 128, 1 + 4 rows, batch 4, context 131072, 16-token pages interleaved",
+        "value": round(gbs, 2), "unit": "GB/s",
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "dtype": "fp16 MFMA operands over the bf16 cache, f32 accumulate and softmax",
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("attn_verify_qwen3_32b"),
+            "kernel": "kv_append_rows_kernel<128> + attn_verify_kernel<128> + "
+                      "attn_verify_combine_kernel<128>",
+            "launch_us_mean": round(float(call_us.mean()), 2),
+            "bytes_per_launch": int(nbytes),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_verify(pool, ids[0], q, k, v, pos, heads, kvh, dim,
+                                                     rows, ctx_len)
+    pool.destroy()
+    backend.close()
+    return result
+
+
+def cpu_baseline_verify(pool, seq, q, k, v, pos, heads, kvh, dim, rows, ctx_len,
+                        sample=16384):
+    """CPU oracle on a bounded sample: the 5 verify rows of sequence 0 over the first
+    `sample` cached tokens (read back from the GPU cache)."""
+    from oracle import pyoracle as O
+
+    keys, vals = pool.read(seq, 0, sample)
+    cache = O.KvCache(kvh * dim, sample + rows, 64, bf16=True)
+    cache.append_many(keys, vals)
+    del keys, vals
+    qn, kn, vn = q[:rows].cpu().numpy(), k[:rows].cpu().numpy(), v[:rows].cpu().numpy()
+    pn = pos[:rows].cpu().numpy().astype(np.int64) - ctx_len + sample
+    nthreads = min(os.cpu_count() or 1, 16)
+    res = {}
+    for threads in (1, nthreads):
+        c = cache.clone()
+        t = time.perf_counter()
+        O.attention_rows(qn, kn, vn, pn, c, heads=heads, kv_heads=kvh, dim=dim, rotary_dim=dim,
+                         theta=1e6, eps=1e-6, threads=threads)
+        res[threads] = time.perf_counter() - t
+    nbytes = sum(sample + j + 1 for j in range(rows)) * kvh * dim * 2 * 2
+    return {"value": round(nbytes / res[1] / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"sequence 0, {rows} verify rows over the first {sample} cached tokens "
+                      f"(bytes counted per row, as bf16)",
+            "ms": round(res[1] * 1e3, 1),
+            "all_cores": {"value": round(nbytes / res[nthreads] / 1e9, 3), "cores": nthreads,
+                          "ms": round(res[nthreads] * 1e3, 1)}}
+
+
 def bench_copy(args, torch):
     """Calibration: a plain device copy of a known size (for PMC byte counters)."""
     nbytes = 1 << 30
@@ -715,8 +859,14 @@ def main():
         result = bench_decode(args, torch, pkg)
         if not args.no_prefill:
             result["prefill"] = bench_prefill(args, torch, pkg, args.prefill_steps, 2)
+            result["verify"] = bench_verify(args, torch, pkg, 5, 2)
             result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 10, 3)
             result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 3, 1)
+    elif args.workload == "verify":
+        result = bench_verify(args, torch, pkg, args.steps, args.warmup)
+        result = {"metric": "MTP verify attention GB/s", "n_gpus": 1, "higher_is_better": True,
+                  "scaling": "weak", "vs_baseline": None, "data": "synthetic",
+                  "config": {"workload": result.pop("workload")}, **result}
     elif args.workload in ("gdn-decode", "gdn-prefill"):
         fn = bench_gdn_decode if args.workload == "gdn-decode" else bench_gdn_prefill
         result = fn(args, torch, pkg, args.steps, args.warmup)

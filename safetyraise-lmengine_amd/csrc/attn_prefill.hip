@@ -288,14 +288,15 @@ struct TileIo {
     bool k_on[KL], v_on[VL];
     const uint16_t *k_pages;
     const uint16_t *v_pages;
-    const int32_t *table;
+    const int32_t *table;  // page ids; entry i is page table_first + i
     size_t head_base;
-    uint32_t lpt, pt_mask, n_keys, n_tiles;
+    uint32_t lpt, pt_mask, n_keys, n_tiles, table_first;
 
     __device__ __forceinline__ void init(int gt, const PrefillParams &p, const BlockPos &b) {
         k_pages = p.k_pages;
         v_pages = p.v_pages;
         table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
+        table_first = 0;
         head_base = (size_t)b.kvh * p.num_pages;
         lpt = p.log2_page_tokens;
         pt_mask = (1u << lpt) - 1;
@@ -330,7 +331,8 @@ struct TileIo {
     }
     __device__ __forceinline__ size_t tok_addr(uint32_t tok) const {
         tok = min(tok, n_keys - 1);  // keys past the block's last row are masked
-        return (((head_base + (uint32_t)table[tok >> lpt]) << lpt) + (tok & pt_mask)) * D;
+        return (((head_base + (uint32_t)table[(tok >> lpt) - table_first]) << lpt) +
+                (tok & pt_mask)) * D;
     }
     __device__ __forceinline__ size_t tile_base(uint32_t t, uint32_t pg) const {
         return (((head_base + pg) << lpt) + ((t * kKeyTile) & pt_mask)) * D;
@@ -930,7 +932,7 @@ hipError_t launch_d(hipStream_t stream, PrefillParams &p, uint32_t g, const SeqM
 // attn_verify_combine_kernel merges (math.rs:133-152 split over the keys).
 // ---------------------------------------------------------------------------
 struct VerifyParams {
-    PrefillParams p;       // meta[s].nblk = partitions of sequence s
+    PrefillParams p;       // meta[s].nblk = records per (row, head) of sequence s
     float *partials;       // records of kRecordStride floats
     uint32_t part_keys;
     uint32_t rows_g;       // query vectors per KV head of the widest sequence (<= 64)
@@ -941,104 +943,230 @@ struct VerifyParams {
 template <int D>
 constexpr int kRecordStride = D + 4;  // m, l, 2 unused, o[D] (16-byte aligned)
 
-// Four waves stage every tile; the waves that hold query vectors (32 each,
-// at most two) also run the products.
+// LDS entries for the page ids of one partition (the host caps part_keys so
+// that a partition never spans more pages)
+constexpr uint32_t kVerifyPageSlots = 2048;
+
+// Tile staging of the verify producers (128 lanes, lane gt): the same LDS
+// images as TileIo (fp16 K rows with k_swz, V^T with vt_swz), but every
+// offset is recomputed from gt at each use, so that only the tiles in flight
+// occupy registers.  Page ids come from the partition's LDS copy.
 template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_verify_kernel(
-    const VerifyParams vp) {
+struct VerifyIo {
+    static constexpr int KCH = D / 8;                       // 16-byte chunks per row
+    static constexpr int KSTEP = 128 / KCH;                 // keys per pass of the lanes
+    static constexpr int KL = kKeyTile / KSTEP;             // K chunks per lane
+    static constexpr int VL = kKeyTile / 4 / KSTEP;         // 4-key V units per lane
+    const uint16_t *k_pages;
+    const uint16_t *v_pages;
+    const int32_t *pids;  // page ids from page `first` on (LDS)
+    size_t head_base;
+    uint32_t lpt, pt_mask, first, last_tok;
+
+    __device__ __forceinline__ size_t row(uint32_t tok) const {
+        tok = min(tok, last_tok);  // keys past the sequence's last are masked
+        return (((head_base + (uint32_t)pids[(tok >> lpt) - first]) << lpt) + (tok & pt_mask)) * D;
+    }
+    __device__ __forceinline__ void load(u32x4 (&kr)[KL], u32x4 (&vr)[4 * VL], uint32_t t,
+                                         uint32_t gt) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            kr[i] = *(const u32x4 *)(k_pages + row(t * kKeyTile + k0 + i * KSTEP) + ch * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < VL; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t key = 4 * (k0 + i * KSTEP) + j;
+                vr[4 * i + j] = *(const u32x4 *)(v_pages + row(t * kKeyTile + key) + ch * 8);
+            }
+    }
+    // valid_keys: keys of the tile that exist; V rows past them become 0
+    __device__ __forceinline__ void store(const u32x4 (&kr)[KL], const u32x4 (&vr)[4 * VL],
+                                          unsigned char *kt, unsigned char *vt,
+                                          uint32_t valid_keys, uint32_t gt) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const uint32_t key = k0 + i * KSTEP;
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(kr[i][j]), bf16hi(kr[i][j]));
+            *(u32x4 *)(kt + key * (D * 2) + ((ch ^ k_swz<D>(key)) * 16)) = f;
+        }
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            const uint32_t g = k0 + i * KSTEP;
+            u32x4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w[j] = (4 * g + j < valid_keys) ? vr[4 * i + j] : u32x4{0, 0, 0, 0};
+            }
+            const uint32_t unit = 2 * (g >> 2) + (g & 1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = ch * 8 + e;
+                const uint32_t lo = pack_f16x2(bf16_elem(w[0], e), bf16_elem(w[1], e));
+                const uint32_t hi = pack_f16x2(bf16_elem(w[2], e), bf16_elem(w[3], e));
+                *(uint2 *)(vt + d * (kKeyTile * 2) + ((unit ^ vt_swz(d)) * 16) +
+                           8 * ((g & 3) >> 1)) = make_uint2(lo, hi);
+            }
+        }
+    }
+};
+
+// One workgroup of 8 waves per (partition, KV head), one workgroup per CU.
+// Waves 4..7 stream the partition's K/V tiles, two per step (lanes 0..127 of
+// the four the even tile, lanes 128..255 the odd one): kVerifyDepth steps
+// are in flight in their registers while they convert the oldest into one
+// of two LDS buffer pairs.  Waves 0..3 are two consumer pairs, one wave per
+// SIMD: pair 0 takes the even tiles, pair 1 the odd ones, each wave of a
+// pair 32 of the query vectors.  One barrier per step: after barrier k, the
+// tiles of step k are in LDS and the buffers of step k-1 are free.  Each
+// pair leaves its own record, so a partition has two.
+constexpr int kVerifyDepth = 2;
+constexpr int kVerifyThreads = 512;
+
+template <int D>
+__global__ __launch_bounds__(kVerifyThreads) __attribute__((amdgpu_waves_per_eu(2))) void
+attn_verify_kernel(const VerifyParams vp) {
     constexpr int NS = D / 16;
     constexpr int NT = D / 32;
-    using Io = TileIo<D, 256, false>;
     extern __shared__ __align__(16) unsigned char lds[];
     const PrefillParams &p = vp.p;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
-    const int h = lane >> 5;
-    const int col = lane & 31;
     const uint32_t kvh = blockIdx.x % p.kv_heads;
     const uint32_t j = blockIdx.x / p.kv_heads;
     uint32_t s = 0;
     while (s + 1 < p.nseq && vp.blk0[s + 1] <= j) ++s;
     const PrefillMeta m = p.meta[s];
     const uint32_t part = j - vp.blk0[s];
-    const uint32_t G = p.heads / p.kv_heads;
-    const uint32_t nvec = m.rows * G;
-    const bool computes = 32u * wave < nvec;               // wave-uniform
-    const uint32_t vec = min(32u * wave + col, nvec - 1);  // this lane's query vector
-    const uint32_t r = vec / G;
-    const uint32_t head = kvh * G + vec % G;
     const uint32_t total = m.ctx + m.rows;
     const uint32_t key_begin = part * vp.part_keys;
     const uint32_t key_end = min(key_begin + vp.part_keys, total);
-    const uint32_t key_limit = m.ctx + r;
-
-    BlockPos b;
-    b.m = m;
-    b.kvh = kvh;
-    b.row0 = 0;
-    b.n_keys = total;
-    b.n_tiles = (total + kKeyTile - 1) / kKeyTile;
-    b.active = true;
-    Io io;
-    io.init(tid, p, b);
-    u32x4 kreg[Io::KL];
-    u32x4 vreg[4 * Io::VL];
     const uint32_t t0 = key_begin / kKeyTile;
     const uint32_t t1 = (key_end + kKeyTile - 1) / kKeyTile;
-    io.load_k(kreg, t0, 0);
-    io.load_v(vreg, t0, 0);
+    // both roles run the same padded number of steps (one barrier each)
+    const uint32_t steps = (t1 - t0 + 1) / 2;
+    const uint32_t k_pad = (steps + kVerifyDepth - 1) / kVerifyDepth * kVerifyDepth;
+    // buffer (step parity b, pair q): K tile, then V^T tile
+    auto tile_lds = [&](uint32_t k, uint32_t q) {
+        return lds + ((k & 1) * 2 + q) * 2 * kTileBytes<D>;
+    };
+
+    if (wave >= 4) {
+        // ---- producers ----
+        const uint32_t pt = tid - 256;  // 0..255
+        const uint32_t q = pt >> 7;     // which tile of the step
+        const uint32_t gt0 = pt & 127;
+        VerifyIo<D> io;
+        io.k_pages = p.k_pages;
+        io.v_pages = p.v_pages;
+        io.head_base = (size_t)kvh * p.num_pages;
+        io.lpt = p.log2_page_tokens;
+        io.pt_mask = (1u << io.lpt) - 1;
+        io.last_tok = total - 1;
+        // the page ids of the partition's keys go to LDS once, so that no
+        // tile load waits on a page-table read
+        int32_t *pids = (int32_t *)(lds + 8 * kTileBytes<D>);
+        const int32_t *table = p.page_table + (size_t)m.slot * p.pages_per_seq;
+        io.first = key_begin >> io.lpt;
+        const uint32_t n = ((key_end - 1) >> io.lpt) - io.first + 1;
+        for (uint32_t i = pt; i < n; i += 256) pids[i] = table[io.first + i];
+        io.pids = pids;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_barrier();  // (A) the producers share pids
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        u32x4 kreg[kVerifyDepth][VerifyIo<D>::KL];
+        u32x4 vreg[kVerifyDepth][4 * VerifyIo<D>::VL];
+#pragma unroll
+        for (int u = 0; u < kVerifyDepth; ++u) {
+            io.load(kreg[u], vreg[u], min(t0 + 2 * u + q, t1 - 1), gt0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (uint32_t kb = 0; kb < k_pad; kb += kVerifyDepth) {
+#pragma unroll
+            for (int u = 0; u < kVerifyDepth; ++u) {
+                // offsets are recomputed from a fresh copy of the lane id
+                // each step instead of being held live across the loop
+                uint32_t gt = gt0;
+                pin(gt);
+                const uint32_t k = kb + u;
+                unsigned char *kt = tile_lds(k, q);
+                // tiles past t1 store a repeat of the last tile nobody reads
+                const uint32_t key0 = min(t0 + 2 * k + q, t1 - 1) * kKeyTile;
+                io.store(kreg[u], vreg[u], kt, kt + kTileBytes<D>, key_end - key0, gt);
+                __syncthreads();  // (B) the tiles of step k are in LDS
+                io.load(kreg[u], vreg[u], min(t0 + 2 * (k + kVerifyDepth) + q, t1 - 1), gt);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        return;
+    }
+
+    // ---- consumers ----
+    const uint32_t pair = wave >> 1;
+    const int cw = wave & 1;  // which 32 query vectors
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const uint32_t G = p.heads / p.kv_heads;
+    const uint32_t nvec = m.rows * G;
+    const bool computes = 32u * cw < nvec;               // wave-uniform
+    const uint32_t vec = min(32u * cw + col, nvec - 1);  // this lane's query vector
+    const uint32_t r = vec / G;
+    const uint32_t head = kvh * G + vec % G;
+    const uint32_t key_limit = m.ctx + r;
     const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
     const size_t qbase = (size_t)(m.row0 + r) * p.heads * hs + (size_t)head * hs;
     f16x8 qop[NS];
     if (computes) q_operands<D>(p, qbase, m.row0 + r, h, lane, qop);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_barrier();  // (A)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
     f32x16 oacc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
     float m_run = -INFINITY;
     float l_run = 0.0f;
-    for (uint32_t t = t0; t < t1; ++t) {
-        unsigned char *kt = lds + (t & 1) * 2 * kTileBytes<D>;
-        unsigned char *vt = kt + kTileBytes<D>;
+    for (uint32_t k = 0; k < k_pad; ++k) {
+        __syncthreads();  // (B)
+        const uint32_t t = t0 + 2 * k + pair;
+        if (!computes || t >= t1) continue;
+        const unsigned char *kt = tile_lds(k, pair);
+        const unsigned char *vt = kt + kTileBytes<D>;
         const uint32_t key0 = t * kKeyTile;
-        io.store_k(kreg, kt);
-        io.store_v(vreg, vt, min(key_end, total) - key0);
-        __syncthreads();
-        if (t + 1 < t1) {
-            io.load_k(kreg, t + 1, 0);
-            io.load_v(vreg, t + 1, 0);
-        }
-        if (computes) {
-            f32x16 sacc[2];
-            s_tile<D>(kt, qop, h, col, sacc);
-            // keys past the partition end (the last tile of the sequence)
-            // and past a row's own position are masked
-            const bool edge = key0 + kKeyTile > min(key_end, m.ctx + 1);
-            if (edge) {
+        f32x16 sacc[2];
+        s_tile<D>(kt, qop, h, col, sacc);
+        // keys past the partition end (the last tile of the sequence) and
+        // past a row's own position are masked
+        const bool edge = key0 + kKeyTile > min(key_end, m.ctx + 1);
+        if (edge) {
 #pragma unroll
-                for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 2; ++u)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
-                        if (key >= key_end) sacc[u][i] = -INFINITY;
-                    }
-            }
-            f16x8 pop[4];
-            softmax_tile<D>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
-            pv_tile<D>(vt, pop, h, col, oacc);
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+                    if (key >= key_end) sacc[u][i] = -INFINITY;
+                }
         }
+        f16x8 pop[4];
+        softmax_tile<D>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
+        pv_tile<D>(vt, pop, h, col, oacc);
     }
     const float l = xhalf_sum(l_run);
-    if (32u * wave + col >= nvec) return;
-    // record of (sequence s, row r, head g, partition): o unnormalised
-    const uint32_t nparts = m.nblk;
+    if (32u * cw + col >= nvec) return;
+    // record (sequence s, row r, head, partition, pair): o unnormalised
+    const uint32_t nrec = m.nblk;  // records per (row, head): two per partition
     float *rec = vp.partials +
-                 ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nparts + part) *
+                 ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nrec + 2 * part + pair) *
                      kRecordStride<D>;
     if (h == 0) {
-        // a partition whose keys are all past this row's limit has l = 0
+        // a pair that saw no key of this row's range has l = 0
         *(float2 *)rec = make_float2(l > 0.0f ? m_run : -INFINITY, l);
     }
 #pragma unroll
@@ -1072,19 +1200,36 @@ __global__ __launch_bounds__(256) void attn_verify_combine_kernel(const VerifyPa
     const uint32_t nparts = m.nblk;
     const float *rec = vp.partials +
                        ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nparts) * kRecordStride<D>;
+    // partition maxima, 64 partitions per pass across the lanes
     float mx = -INFINITY;
-    for (uint32_t q = 0; q < nparts; ++q) mx = fmaxf(mx, rec[(size_t)q * kRecordStride<D>]);
+    for (uint32_t q = lane; q < nparts; q += 64) mx = fmaxf(mx, rec[(size_t)q * kRecordStride<D>]);
+    mx = max64(mx);
     float l = 0.0f;
     float o[EPL] = {};
-    for (uint32_t q = 0; q < nparts; ++q) {
-        const float *rq = rec + (size_t)q * kRecordStride<D>;
-        const float mq = rq[0];
-        if (mq == -INFINITY) continue;  // no visible key in this partition
-        const float sc = fast_exp2(mq - mx);
-        l += rq[1] * sc;
+    for (uint32_t q0 = 0; q0 < nparts; q0 += 64) {
+        // lane j holds the weight of partition q0 + j; a partition with no
+        // visible key (m = -inf) has weight 0 and its o is never read
+        float sc = 0.0f;
+        if (q0 + lane < nparts) {
+            const float2 ml = *(const float2 *)(rec + (size_t)(q0 + lane) * kRecordStride<D>);
+            if (ml.x != -INFINITY) {
+                sc = fast_exp2(ml.x - mx);
+                l += ml.y * sc;
+            }
+        }
+        const uint32_t n = min(64u, nparts - q0);
+#pragma unroll 4
+        for (uint32_t j = 0; j < n; ++j) {
+            const float w = __shfl(sc, (int)j);
+            const float *rq = rec + (size_t)(q0 + j) * kRecordStride<D> + 4;
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) o[i] += rq[4 + lane + 64 * i] * sc;
+            for (int i = 0; i < EPL; ++i) {
+                const float x = rq[lane + 64 * i];
+                o[i] += w != 0.0f ? x * w : 0.0f;
+            }
+        }
     }
+    l = sum64(l);
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
     const uint32_t hs = gated ? 2 * D : D;
@@ -1106,7 +1251,7 @@ template <int D>
 hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
                            uint32_t combine_waves) {
     static bool configured = false;
-    const size_t lds = 4 * kTileBytes<D>;
+    const size_t lds = 8 * kTileBytes<D> + kVerifyPageSlots * sizeof(int32_t);
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute((const void *)attn_verify_kernel<D>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1114,7 +1259,8 @@ hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(attn_verify_kernel<D>, dim3(blocks), dim3(256), lds, stream, vp);
+    hipLaunchKernelGGL(attn_verify_kernel<D>, dim3(blocks), dim3(kVerifyThreads), lds, stream,
+                       vp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(attn_verify_combine_kernel<D>, dim3((combine_waves + 3) / 4), dim3(256), 0,
@@ -1192,8 +1338,8 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
     VerifyParams vp{};
     vp.p = fill_params(a, nseq, rope_scratch);
     PrefillParams &p = vp.p;
-    // partition size: about 2 workgroups per CU over the whole call, at
-    // least 256 keys, a multiple of the 64-key tile
+    // partition size: one workgroup per CU over the whole call, at least
+    // 256 keys, a multiple of the 64-key tile
     uint64_t keys = 0;
     uint32_t max_rows = 0, rows_g = 0;
     for (int i = 0; i < nseq; ++i) {
@@ -1202,10 +1348,13 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         max_rows = std::max(max_rows, seqs[i].rows);
         rows_g = std::max(rows_g, seqs[i].rows * g);
     }
-    const uint64_t target = (uint64_t)std::max(in.num_cus, 1) * 2;
+    const uint64_t target = (uint64_t)std::max(in.num_cus, 1);
     uint64_t part = (keys * a.kv_heads + target - 1) / target;
     part = std::max<uint64_t>(256, (part + kKeyTile - 1) / kKeyTile * kKeyTile);
-    vp.part_keys = (uint32_t)std::min<uint64_t>(part, 1u << 30);
+    // a partition starting mid-page touches at most part/page_tokens + 2 pages
+    const uint64_t max_part =
+        ((uint64_t)(kVerifyPageSlots - 2) * a.pool->page_tokens) / kKeyTile * kKeyTile;
+    vp.part_keys = (uint32_t)std::min<uint64_t>(std::min(part, max_part), 1u << 30);
     vp.rows_g = rows_g;
     uint32_t blocks = 0, records = 0, waves = 0;
     for (int i = 0; i < nseq; ++i) {
@@ -1214,10 +1363,11 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         m.ctx = seqs[i].ctx;
         m.rows = seqs[i].rows;
         m.row0 = seqs[i].row0;
-        m.nblk = (m.ctx + m.rows + vp.part_keys - 1) / vp.part_keys;
+        const uint32_t parts = (m.ctx + m.rows + vp.part_keys - 1) / vp.part_keys;
+        m.nblk = 2 * parts;  // records per (row, head): one per consumer pair
         vp.blk0[i] = blocks;
         vp.rec0[i] = records;
-        blocks += m.nblk;
+        blocks += parts;
         records += m.nblk * m.rows * a.heads;
         waves += m.rows * a.heads;
     }
