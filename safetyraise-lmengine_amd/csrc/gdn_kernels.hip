@@ -76,8 +76,14 @@ struct ConvChan {
 #pragma unroll
         for (int j = 0; j < kMaxK; ++j) w[j] = weights[j < (int)K - 1 ? j : (int)K - 1];
     }
+    static constexpr int kK = 0;  // kernel size known only at run time
     // silu(sum_{j<K-1} hist[j] * w[j] + x * w[K-1]), then append x
     __device__ __forceinline__ float step(float x, uint32_t K) {
+        const float value = pre(x, K);
+        return value * ref_sigmoid(value);
+    }
+    // the conv sum before silu, then append x
+    __device__ __forceinline__ float pre(float x, uint32_t K) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < kMaxK - 1; ++j) {
@@ -94,7 +100,7 @@ struct ConvChan {
             if (j + 2 < (int)K) hist[j] = hist[j + 1];
             else if (j + 2 == (int)K) hist[j] = x;
         }
-        return value * ref_sigmoid(value);
+        return value;
     }
     __device__ __forceinline__ void store(float *history_row, uint32_t K) const {
 #pragma unroll
@@ -401,6 +407,614 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(p.history + (hist_next + ch1) * K1, p.conv_k);
 }
 
+// ---------------------------------------------------------------------------
+// gdn_chunk_kernel: the delta rule of prefill-sized calls in chunked form on
+// f32 MFMA (v_mfma_f32_16x16x4f32).  With k^, q^ the L2-normalised conv
+// outputs, g_t = sum_{i<=t} log(alpha_i) over the chunk and S0 the state at
+// the chunk start, the token-serial recurrence (math.rs:222-236)
+//     S_t = alpha_t S_{t-1} + delta_t k^_t^T,
+//     delta_t = beta_t (v_t - alpha_t S_{t-1} k^_t)
+// unrolls to S_t = e^{g_t} S0 + sum_{j<=t} e^{g_t-g_j} delta_j k^_j^T, and
+// the deltas of a chunk solve the unit lower-triangular system
+//     (I + A) Delta = diag(beta) V - diag(beta e^g) K^ S0^T,
+//     A[t][j] = beta_t e^{g_t-g_j} (k^_t . k^_j)  (j < t),
+// so with T = (I + A)^-1, W = T diag(beta e^g) K^, U = T diag(beta) V:
+//     Delta = U - W S0^T
+//     o_t   = (e^{g_t} S0 q^_t + sum_{j<=t} e^{g_t-g_j} (q^_t . k^_j) delta_j) / sqrt(Dk)
+//     S_C   = e^{g_C} S0 + sum_j e^{g_C-g_j} delta_j k^_j^T.
+// Decays enter only as e^{x} with x <= 0.  One workgroup per (sequence,
+// value head, 32 of the Dv = 128 state rows): rows of S are independent, so
+// the state slice stays in LDS for all chunks of the call; the chunk-wide
+// products (q.k, k.k, T, W) are recomputed by the four workgroups of a head.
+// The conv history is double-buffered exactly as in gdn_delta_kernel.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ void pin(T &x) {
+    asm volatile("" : "+v"(x));
+}
+
+constexpr int kCk = 32;        // rows per chunk
+constexpr int kVs = 32;        // state rows (value dims) per workgroup
+constexpr int kPr = kDk + 4;   // pitch (floats) of [.][Dk] arrays
+constexpr int kPc = kCk + 4;   // pitch of [.][chunk] arrays
+constexpr int kChunkThreads = 256;
+constexpr int kXin = 2 * kDk + kVs;  // conv channels a workgroup reads
+
+// x * sigmoid(x) with the hardware exp2 and reciprocal (a few ulp from the
+// libm form; the chunked path is held to the f32 tolerance, not to ulps)
+__device__ __forceinline__ float fast_silu(float x) {
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+struct ChunkLds {
+    float s0[kVs][kPr];   // state slice: rows v, dims d
+    float q[kCk][kPr];    // conv(q) rows t; later -W
+    float k[kCk][kPr];    // conv(k) rows t
+    float kc[kDk][kPc];   // conv(k) transposed: [d][t]
+    float vc[kVs][kPc];   // conv(v) of the slice transposed: [v][t]
+    float a[kCk][kPc];    // A (strictly lower)
+    float t[kCk][kPc];    // T = (I + A)^-1
+    float pm[kCk][kPc];   // e^{g_t-g_j} (q^_t . k^_j), j <= t
+    float dt[kVs][kPc];   // Delta transposed: [v][t]
+    float g[kCk];         // cumulative log decay
+    float beta[kCk];
+    float rq[kCk];        // 1 / |q_t|
+    float rk[kCk];        // 1 / |k_t|
+    float sw[kCk];        // column scales of T: beta_j e^{g_j} / |k_j| (W)
+    float su[kCk];        //   beta_j (U)
+    float ss[kCk];        //   e^{g_C - g_j} / |k_j| (state update; g_C: last row)
+    float xin[kCk][kXin]; // raw conv inputs of the chunk: q, k, then the v slice
+};
+
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One lane's operand of a 16-row tile over NK steps of 16 k: row lane & 15,
+// k = 16 s + 4 (lane >> 4) + i.  The tile's rows are k-contiguous in LDS.
+// Every product below is acc += A . B^T with both operands in this form;
+// the i-th MFMA of a step takes element i, so lane (r, slot) feeds A row r
+// and B row r at the same k, and the tile's rows 4 slot + i, column r are
+// acc[i].  All reads of an operand are issued before any MFMA uses them.
+template <int NK>
+struct Ops {
+    f32x4 v[NK];
+};
+
+template <int NK>
+__device__ __forceinline__ void load_ops(Ops<NK> &o, const float *row0, int ld, int lane) {
+    const float *p = row0 + (lane & 15) * ld + 4 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < NK; ++s) o.v[s] = *(const f32x4 *)(p + 16 * s);
+}
+
+// multiplies the operand's k-th element by scale[k]
+template <int NK>
+__device__ __forceinline__ void scale_ops(Ops<NK> &o, const float *scale, int lane) {
+    const float *p = scale + 4 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+        o.v[s] *= *(const f32x4 *)(p + 16 * s);
+    }
+}
+
+template <int NK>
+__device__ __forceinline__ void mma(f32x4 &acc, const Ops<NK> &a, const Ops<NK> &b) {
+#pragma unroll
+    for (int s = 0; s < NK; ++s) {
+        acc = mfma4(a.v[s].x, b.v[s].x, acc);
+        acc = mfma4(a.v[s].y, b.v[s].y, acc);
+        acc = mfma4(a.v[s].z, b.v[s].z, acc);
+        acc = mfma4(a.v[s].w, b.v[s].w, acc);
+    }
+}
+
+// Causal conv channel with the kernel size K known at compile time; same
+// arithmetic and history layout as ConvChan.
+template <int K>
+struct ConvK {
+    static constexpr int kK = K;
+    static constexpr int H = K > 1 ? K - 1 : 1;
+    float hist[H];
+    float w[K];
+    __device__ __forceinline__ void load(const float *history_row, const float *weights,
+                                         uint32_t) {
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) hist[j] = history_row[j];
+#pragma unroll
+        for (int j = 0; j < K; ++j) w[j] = weights[j];
+    }
+    __device__ __forceinline__ float pre(float x, uint32_t) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) acc += hist[j] * w[j];
+        const float value = acc + x * w[K - 1];
+#pragma unroll
+        for (int j = 0; j + 1 < K - 1; ++j) hist[j] = hist[j + 1];
+        if constexpr (K > 1) hist[K - 2] = x;
+        return value;
+    }
+    __device__ __forceinline__ void store(float *history_row, uint32_t) const {
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) history_row[j] = hist[j];
+    }
+};
+
+// a[i] for a run-time i, as selects (a dynamically indexed register array
+// would live in scratch memory)
+template <int N>
+__device__ __forceinline__ float pick(const float (&a)[N], int i) {
+    float x = a[0];
+#pragma unroll
+    for (int j = 1; j < N; ++j) x = i == j ? a[j] : x;
+    return x;
+}
+
+template <class Conv>
+__global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParams p) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    ChunkLds &L = *(ChunkLds *)lds_raw;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r16 = lane & 15;
+    const int sl = lane >> 4;
+    const int tr = wave >> 1, tc = wave & 1;  // this wave's tile of the products
+
+    const uint32_t nq = p.value_dim / kVs;  // state-row blocks per head
+    const uint32_t vq = blockIdx.x % nq;
+    const uint32_t h = (blockIdx.x / nq) % p.value_heads;
+    const GdnMeta m = p.meta[blockIdx.x / (nq * p.value_heads)];
+    const uint32_t groups = p.value_heads / p.key_heads;
+    const uint32_t kh = h / groups;
+    const uint32_t key_width = p.key_heads * kDk;
+    const uint32_t K1 = p.conv_k - 1;
+    const bool bf16_in = p.bf16_in != 0;
+
+    // conv channels: thread tid < 128 q dim tid, tid < 256 k dim tid - 128,
+    // over all rows of a chunk; lanes 0..31 of every wave also the 32 v
+    // channels of the slice over their wave's 8 rows of the chunk
+    constexpr int KC = Conv::kK;                   // 0: run-time kernel size
+    constexpr int KW = KC ? KC : kMaxK;            // window bound
+    const int Kr = KC ? KC : (int)p.conv_k;
+    const uint32_t ch0 = tid < kDk ? kh * kDk + tid : key_width + kh * kDk + (tid - kDk);
+    const int cvl = lane & 31;
+    const uint32_t ch1 = 2 * key_width + h * p.value_dim + vq * kVs + cvl;
+    const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
+    const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
+    Conv cv0;
+    cv0.load(p.history + (hist_slot + ch0) * K1, p.conv_w + (size_t)ch0 * p.conv_k, p.conv_k);
+    // the v channel: weights and the K-1 inputs before the chunk
+    float wv[KW], hv[KW > 1 ? KW - 1 : 1];
+#pragma unroll
+    for (int j = 0; j < KW; ++j) wv[j] = p.conv_w[(size_t)ch1 * p.conv_k + min(j, Kr - 1)];
+#pragma unroll
+    for (int j = 0; j < KW - 1; ++j) hv[j] = p.history[(hist_slot + ch1) * K1 + min(j, max(Kr - 2, 0))];
+
+    // state slice -> LDS (16 floats per thread)
+    float *state = p.state + (((size_t)m.slot * p.value_heads + h) * p.value_dim + vq * kVs) * kDk;
+    {
+        const int v = tid >> 3, d0 = (tid & 7) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *(float4 *)&L.s0[v][d0 + 4 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 4 * i);
+        }
+    }
+    const float a_log_e = expf(p.a_log[h]);
+    const float dt_bias = p.dt_bias[h];
+    const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
+
+    for (uint32_t r0 = 0; r0 < m.rows; r0 += kCk) {
+        const uint32_t nv = min((uint32_t)kCk, m.rows - r0);
+        const size_t row0 = (size_t)m.row0 + r0;
+        // ---- raw inputs of the chunk -> LDS in 16-byte segments of the
+        //      three channel ranges (q, k of the key head; the v slice), every
+        //      load in flight together; rows past nv repeat the last valid
+        //      row and are not used.  The lane id is re-pinned per chunk so
+        //      that the segment offsets are recomputed, not held live.
+        {
+            uint32_t lt = tid;
+            pin(lt);
+            auto seg_src = [&](int t, int c0) -> size_t {
+                const uint32_t ch = c0 < kDk ? kh * kDk + c0
+                                  : c0 < 2 * kDk ? key_width + kh * kDk + (c0 - kDk)
+                                                 : 2 * key_width + h * p.value_dim + vq * kVs + (c0 - 2 * kDk);
+                return (row0 + min((uint32_t)t, nv - 1)) * p.channels + ch;
+            };
+            if (!bf16_in) {
+                constexpr int SEG = kXin / 4;                       // per row
+                constexpr int N = kCk * SEG / kChunkThreads;        // per thread
+                static_assert(kCk * SEG % kChunkThreads == 0, "segments");
+                f32x4 xs[N];
+#pragma unroll
+                for (int n = 0; n < N; ++n) {
+                    const int e = lt + n * kChunkThreads;
+                    xs[n] = *(const f32x4 *)((const float *)p.qkv + seg_src(e / SEG, 4 * (e % SEG)));
+                }
+#pragma unroll
+                for (int n = 0; n < N; ++n) {
+                    const int e = lt + n * kChunkThreads;
+                    *(f32x4 *)&L.xin[e / SEG][4 * (e % SEG)] = xs[n];
+                }
+            } else {
+                constexpr int SEG = kXin / 8;
+                constexpr int N = (kCk * SEG + kChunkThreads - 1) / kChunkThreads;
+                u32x4 xs[N];
+#pragma unroll
+                for (int n = 0; n < N; ++n) {
+                    const int e = min((int)lt + n * kChunkThreads, kCk * SEG - 1);
+                    xs[n] = *(const u32x4 *)((const uint16_t *)p.qkv + seg_src(e / SEG, 8 * (e % SEG)));
+                }
+#pragma unroll
+                for (int n = 0; n < N; ++n) {
+                    const int e = (int)lt + n * kChunkThreads;
+                    if (e < kCk * SEG) {
+                        float *dst = &L.xin[e / SEG][8 * (e % SEG)];
+                        *(f32x4 *)dst = f32x4{__uint_as_float(xs[n][0] << 16), __uint_as_float(xs[n][0] & 0xffff0000u),
+                                              __uint_as_float(xs[n][1] << 16), __uint_as_float(xs[n][1] & 0xffff0000u)};
+                        *(f32x4 *)(dst + 4) = f32x4{__uint_as_float(xs[n][2] << 16), __uint_as_float(xs[n][2] & 0xffff0000u),
+                                                    __uint_as_float(xs[n][3] << 16), __uint_as_float(xs[n][3] & 0xffff0000u)};
+                    }
+                }
+            }
+        }
+        float av = 0.0f, bv = 0.0f;
+        {
+            const size_t row = row0 + min((uint32_t)cvl, nv - 1);
+            av = load_act_nb(p.a, row * p.value_heads + h, bf16_in);
+            bv = load_act_nb(p.b, row * p.value_heads + h, bf16_in);
+        }
+        __syncthreads();
+        // ---- causal conv + silu (math.rs:158-187); rows past nv are zero
+        //      and do not advance the history.  Each phase reads its LDS
+        //      inputs into registers first, then computes, then stores.
+        const bool full = nv == (uint32_t)kCk;
+        {
+            float xr[kCk];
+#pragma unroll
+            for (int t = 0; t < kCk; ++t) xr[t] = L.xin[t][tid];
+            float yr[kCk];
+            if (full) {
+#pragma unroll
+                for (int t = 0; t < kCk; ++t) yr[t] = fast_silu(cv0.pre(xr[t], p.conv_k));
+            } else {
+#pragma unroll
+                for (int t = 0; t < kCk; ++t) {
+                    yr[t] = 0.0f;
+                    if ((uint32_t)t < nv) yr[t] = fast_silu(cv0.pre(xr[t], p.conv_k));
+                }
+            }
+            if (tid < kDk) {
+#pragma unroll
+                for (int t = 0; t < kCk; ++t) L.q[t][tid] = yr[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < kCk; ++t) L.k[t][tid - kDk] = yr[t];
+#pragma unroll
+                for (int t = 0; t < kCk; t += 4) {
+                    *(f32x4 *)&L.kc[tid - kDk][t] = f32x4{yr[t], yr[t + 1], yr[t + 2], yr[t + 3]};
+                }
+            }
+        }
+        {
+            // v channel cvl, rows tb .. tb + 7 (tb = 8 wave): the window of
+            // row t is position t + j (tap j) of (hv, x_0, x_1, ...); only
+            // wave 0's rows reach into hv
+            const int tb = 8 * wave;
+            constexpr int NW = 8 + KW - 1;
+            float xw[NW];  // positions tb .. tb + NW - 1 of (hv, x)
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const int u = tb + i - (Kr - 1);  // input row
+                xw[i] = L.xin[min(max(u, 0), kCk - 1)][2 * kDk + cvl];
+                if (wave == 0 && i < KW - 1) {
+                    if (i < Kr - 1) xw[i] = hv[i < KW - 1 ? i : 0];
+                }
+            }
+            float yv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < KW; ++j) {
+                    if (j < Kr) acc += xw[i + j] * wv[j];
+                }
+                yv[i] = (uint32_t)(tb + i) < nv ? fast_silu(acc) : 0.0f;
+            }
+            if (lane < kVs) {
+                *(f32x4 *)&L.vc[lane][tb] = f32x4{yv[0], yv[1], yv[2], yv[3]};
+                *(f32x4 *)&L.vc[lane][tb + 4] = f32x4{yv[4], yv[5], yv[6], yv[7]};
+            }
+            // the history after the chunk: the last K-1 of (hv, x_0 .. x_{nv-1})
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < KW - 1; ++j) {
+                    if (j < Kr - 1) hv[j] = L.xin[kCk - (Kr - 1) + j][2 * kDk + cvl];
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < kCk; ++t) {
+                    if ((uint32_t)t < nv) {
+                        const float x = L.xin[t][2 * kDk + cvl];
+#pragma unroll
+                        for (int j = 0; j < KW - 1; ++j) {
+                            if (j + 2 < Kr) hv[j] = hv[j + 1];
+                            else if (j + 2 == Kr) hv[j] = x;
+                        }
+                    }
+                }
+            }
+        }
+        if (wave == 1) {
+            // decay and write strength (math.rs:220-221); padded rows: alpha 1, beta 0
+            const bool valid = (uint32_t)cvl < nv;
+            float la = valid ? -a_log_e * softplus_ref(av + dt_bias) : 0.0f;
+            const float beta = valid ? ref_sigmoid(bv) : 0.0f;
+#pragma unroll
+            for (int o = 1; o < kCk; o <<= 1) {
+                const float y = __shfl_up(la, o);
+                if (cvl >= o) la += y;
+            }
+            if (lane < kCk) {
+                L.g[lane] = la;
+                L.beta[lane] = beta;
+            }
+        }
+        __syncthreads();
+        // ---- L2 norms of q and k per row (math.rs:218-219): 8 lanes per
+        //      row, 16 dims each, then a reduction over the 8
+        {
+            const int t = 8 * wave + (lane >> 3), part = lane & 7;
+            float sq = 0.0f, sk = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 a4 = *(const float4 *)&L.q[t][16 * part + 4 * i];
+                const float4 b4 = *(const float4 *)&L.k[t][16 * part + 4 * i];
+                sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
+                sk += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
+            }
+#pragma unroll
+            for (int o = 1; o < 8; o <<= 1) {
+                sq += __shfl_xor(sq, o);
+                sk += __shfl_xor(sk, o);
+            }
+            if (part == 0) {
+                L.rq[t] = 1.0f / sqrtf(sq + 1e-6f);
+                L.rk[t] = 1.0f / sqrtf(sk + 1e-6f);
+            }
+        }
+        __syncthreads();
+        // ---- P1: q.k, k.k and q.S0 tiles; wave w owns tile (w >> 1, w & 1)
+        //      (the three accumulation chains interleaved)
+        f32x4 oq = {0, 0, 0, 0};
+        {
+            f32x4 sqk = {0, 0, 0, 0}, akk = {0, 0, 0, 0};
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+            constexpr int NH = kDk / 32;
+            Ops<NH> qa, kb, sb, ka;
+            load_ops(qa, &L.q[16 * tr][NH * 16 * half], kPr, lane);
+            load_ops(kb, &L.k[16 * tc][NH * 16 * half], kPr, lane);
+            load_ops(sb, &L.s0[16 * tc][NH * 16 * half], kPr, lane);
+            load_ops(ka, &L.k[16 * tr][NH * 16 * half], kPr, lane);
+#pragma unroll
+            for (int st = 0; st < NH; ++st) {
+                sqk = mfma4(qa.v[st].x, kb.v[st].x, sqk);
+                oq = mfma4(qa.v[st].x, sb.v[st].x, oq);
+                akk = mfma4(ka.v[st].x, kb.v[st].x, akk);
+                sqk = mfma4(qa.v[st].y, kb.v[st].y, sqk);
+                oq = mfma4(qa.v[st].y, sb.v[st].y, oq);
+                akk = mfma4(ka.v[st].y, kb.v[st].y, akk);
+                sqk = mfma4(qa.v[st].z, kb.v[st].z, sqk);
+                oq = mfma4(qa.v[st].z, sb.v[st].z, oq);
+                akk = mfma4(ka.v[st].z, kb.v[st].z, akk);
+                sqk = mfma4(qa.v[st].w, kb.v[st].w, sqk);
+                oq = mfma4(qa.v[st].w, sb.v[st].w, oq);
+                akk = mfma4(ka.v[st].w, kb.v[st].w, akk);
+            }
+            }
+            const int j = 16 * tc + r16;
+            const float gj = L.g[j], rkj = L.rk[j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * tr + 4 * sl + i;
+                const float gt = L.g[t];
+                const float e = expf(j <= t ? gt - gj : -INFINITY);
+                L.pm[t][j] = e * L.rq[t] * rkj * sqk[i];
+                L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * akk[i] : 0.0f;
+                oq[i] *= L.rq[t] * expf(gt);  // e^{g_t} S0 q^_t
+            }
+        }
+        __syncthreads();
+        // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
+        //      blocks by forward substitution (lane j: column j), storing T
+        //      and its transpose; wave 2 clears the upper-right block and
+        //      wave 3 computes the column scales.
+        if (wave < 2) {
+            const int b0 = 16 * wave;
+            const int j = r16;
+            // the block's strict lower triangle, in registers first
+            f32x4 ar[16][4];
+#pragma unroll
+            for (int i = 1; i < 16; ++i)
+#pragma unroll
+                for (int qd = 0; 4 * qd < i; ++qd) ar[i][qd] = *(const f32x4 *)&L.a[b0 + i][b0 + 4 * qd];
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float acc0 = i == j ? 1.0f : 0.0f, acc1 = 0.0f;
+#pragma unroll
+                for (int mm = 0; mm < i; ++mm) {
+                    const float am = ar[i][mm >> 2][mm & 3];
+                    if (mm & 1) acc1 -= am * x[mm];
+                    else acc0 -= am * x[mm];
+                }
+                x[i] = acc0 + acc1;
+            }
+            if (lane < 16) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    L.t[b0 + i][b0 + j] = x[i];
+                    L.dt[b0 + j][b0 + i] = x[i];  // T^T (dt is free until P4)
+                }
+            }
+        } else if (wave == 2) {
+            for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
+        } else if (lane < kCk) {
+            // W uses beta_j e^{g_j} / |k_j|, U beta_j, the state update
+            // e^{g_C - g_j} / |k_j| (g_C: the last row's g)
+            const float gj = L.g[lane], rkj = L.rk[lane];
+            L.sw[lane] = L.beta[lane] * expf(gj) * rkj;
+            L.su[lane] = L.beta[lane];
+            L.ss[lane] = expf(L.g[kCk - 1] - gj) * rkj;
+        }
+        __syncthreads();
+        //      T21 = -T22 A21 T11 (wave 0): M = A21 T11 with B = T11^T rows,
+        //      M^T through LDS (pm rows are read only in P5; use a scratch
+        //      block of dt), then T21 = -T22 M.
+        if (wave == 0) {
+            Ops<1> a21, t11t;
+            load_ops(a21, &L.a[16][0], kPc, lane);
+            load_ops(t11t, &L.dt[0][0], kPc, lane);
+            f32x4 mt = {0, 0, 0, 0};
+            mma(mt, a21, t11t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.dt[16 + r16][4 * sl + i] = mt[i];  // M^T
+            Ops<1> t22, mtr;
+            load_ops(t22, &L.t[16][16], kPc, lane);
+            load_ops(mtr, &L.dt[16][0], kPc, lane);
+            f32x4 t21 = {0, 0, 0, 0};
+            mma(t21, t22, mtr);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
+        }
+        __syncthreads();
+        // ---- P3: W = T diag(sw) K (stored negated over q, which nobody
+        //      reads after P1) and U = T diag(su) V (this wave's Delta
+        //      accumulator)
+        f32x4 du = {0, 0, 0, 0};
+        {
+            Ops<2> tw, tu, vb;
+            load_ops(tw, &L.t[16 * tr][0], kPc, lane);
+            tu = tw;
+            load_ops(vb, &L.vc[16 * tc][0], kPc, lane);
+            Ops<2> kb4[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &L.kc[64 * tc + 16 * n][0], kPc, lane);
+            scale_ops(tw, L.sw, lane);
+            scale_ops(tu, L.su, lane);
+            f32x4 w[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    du = mfma4(tu.v[st][e], vb.v[st][e], du);
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) w[n] = mfma4(tw.v[st][e], kb4[n].v[st][e], w[n]);
+                }
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) L.q[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = -w[n][i];
+        }
+        __syncthreads();
+        // ---- P4: Delta = U - W S0^T; stored transposed
+        {
+            Ops<kDk / 16> wa, sb;
+            load_ops(wa, &L.q[16 * tr][0], kPr, lane);
+            load_ops(sb, &L.s0[16 * tc][0], kPr, lane);
+            f32x4 d2 = {0, 0, 0, 0};
+#pragma unroll
+            for (int st = 0; st < kDk / 16; ++st)
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    du = mfma4(wa.v[st][e], sb.v[st][e], du);
+                    d2 = mfma4(wa.v[st][e + 1], sb.v[st][e + 1], d2);
+                }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.dt[16 * tc + r16][16 * tr + 4 * sl + i] = du[i] + d2[i];
+        }
+        __syncthreads();
+        // ---- P5: outputs, then the state at the chunk end
+        {
+            Ops<2> pa, db, da;
+            load_ops(pa, &L.pm[16 * tr][0], kPc, lane);
+            load_ops(db, &L.dt[16 * tc][0], kPc, lane);
+            load_ops(da, &L.dt[16 * tr][0], kPc, lane);
+            Ops<2> kb4[4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &L.kc[64 * tc + 16 * n][0], kPc, lane);
+            float s0v[4][4];
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s0v[n][i] = L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16];
+            scale_ops(da, L.ss, lane);
+            f32x4 s4[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    oq = mfma4(pa.v[st][e], db.v[st][e], oq);
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) s4[n] = mfma4(da.v[st][e], kb4[n].v[st][e], s4[n]);
+                }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = 16 * tr + 4 * sl + i;
+                if (t < nv) {
+                    p.raw_out[(row0 + t) * p.value_heads * p.value_dim + (size_t)h * p.value_dim +
+                              vq * kVs + 16 * tc + r16] = oq[i] * qscale;
+                }
+            }
+            const float eC = expf(L.g[kCk - 1]);
+            __syncthreads();  // all reads of S0 are done
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = s4[n][i] + eC * s0v[n][i];
+                }
+            __syncthreads();  // the next chunk reads S0 and rewrites q, k, pm, ...
+        }
+    }
+    // state slice and history back
+    {
+        const int v = tid >> 3, d0 = (tid & 7) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *(float4 *)(state + (size_t)v * kDk + d0 + 4 * i) = *(const float4 *)&L.s0[v][d0 + 4 * i];
+        }
+    }
+    const bool owns_qk = (h % groups == 0) && vq == 0;
+    if (owns_qk) cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
+    if (wave == 0 && lane < kVs) {
+#pragma unroll
+        for (int j = 0; j < KW - 1; ++j) {
+            if (j < Kr - 1) p.history[(hist_next + ch1) * K1 + j] = hv[j];
+        }
+    }
+}
+
+template <class Conv>
+hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t blocks) {
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_kernel<Conv>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)sizeof(ChunkLds));
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(gdn_chunk_kernel<Conv>, dim3(blocks), dim3(kChunkThreads), sizeof(ChunkLds),
+                       stream, p);
+    return hipGetLastError();
+}
+
 struct NormParams {
     const float *raw;   // [rows][Hv*Dv]
     const void *z;      // [rows][Hv*Dv]
@@ -446,6 +1060,10 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
     uint32_t max_rows = 0;
     for (int i = 0; i < nseq; ++i) max_rows = rows[i] > max_rows ? rows[i] : max_rows;
     const bool head_kernel = pool->value_dim == kHeadDv && max_rows <= kHeadKernelRows;
+    // longer calls with Dv = 128 take the chunked MFMA form (which reads the
+    // qkv rows in 16-byte segments)
+    const bool chunk_kernel = pool->value_dim == kHeadDv && !head_kernel &&
+                              ((uintptr_t)g.qkv & 15) == 0;
     for (int base = 0; base < nseq; base += kMetaPerLaunch) {
         const int n = (nseq - base) < kMetaPerLaunch ? (nseq - base) : kMetaPerLaunch;
         GdnParams p;
@@ -473,6 +1091,11 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
             const uint32_t blocks = (uint32_t)n * pool->value_heads;
             hipLaunchKernelGGL(gdn_head_kernel<kHeadThreads>, dim3(blocks), dim3(kHeadThreads), 0,
                                stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
+        } else if (chunk_kernel) {
+            const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kVs);
+            const hipError_t e = p.conv_k == 4 ? launch_chunk<ConvK<4>>(stream, p, blocks)
+                                               : launch_chunk<ConvChan>(stream, p, blocks);
+            if (e != hipSuccess) return e;
         } else {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kRows);
             hipLaunchKernelGGL(gdn_delta_kernel, dim3(blocks), dim3(kThreads), 0, stream, p);

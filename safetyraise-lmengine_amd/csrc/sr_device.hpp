@@ -109,13 +109,12 @@ __device__ __forceinline__ int rope_axis(uint32_t i, const uint32_t mrope[3], bo
     return 2;
 }
 
-// Reference sigmoid (src/model/math.rs:11-18).
+// Reference sigmoid (src/model/math.rs:11-18): 1 / (1 + e^-x) for x >= 0,
+// e^x / (1 + e^x) otherwise.  Both branches share e = e^{-|x|}, so one exp
+// and one division give the same values without divergence.
 __device__ __forceinline__ float ref_sigmoid(float x) {
-    if (x >= 0.0f) {
-        return 1.0f / (1.0f + expf(-x));
-    }
-    const float e = expf(x);
-    return e / (1.0f + e);
+    const float e = expf(-fabsf(x));
+    return (x >= 0.0f ? 1.0f : e) / (1.0f + e);
 }
 
 }  // namespace sr

@@ -158,3 +158,82 @@ def test_gdn_error_paths(pkg, backend, rng):
     with pytest.raises(pkg.PluginError):
         plugin_rows(pkg, backend, pool, L, [s + 1], [1], L.inputs(rng, 1))
     pool.destroy()
+
+
+def run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, what):
+    """One call over several sequences; each checked against the oracle
+    (outputs, then the states and histories the oracle carried)."""
+    xs = [L.inputs(rng, n) for n in rows]
+    x = tuple(np.concatenate(parts) for parts in zip(*xs))
+    got = plugin_rows(pkg, backend, pool, L, seqs, rows, x)
+    off = 0
+    for i, (n, (m, h)) in enumerate(zip(rows, refs)):
+        close(got[off:off + n], oracle_rows(L, xs[i], m, h), what=f"{what} seq {i} ({n} rows)")
+        off += n
+    for i, (s, (m, h)) in enumerate(zip(seqs, refs)):
+        gm, gh = pool.read(s)
+        close(gm, m, what=f"{what} state {i}")
+        close(gh, h, atol=0, rtol=0, what=f"{what} history {i}")
+
+
+def test_gdn_chunked_form_ragged_rows_seeded_state(pkg, backend, rng):
+    # calls with more than 8 rows run the chunked (WY) form in chunks of 32:
+    # full, partial and multi-chunk sequences next to a decode row, from
+    # seeded states, over consecutive calls; non-zero A_log and dt_bias
+    L = Layer(rng, 16, 32)
+    L.a_log = (0.3 * rng.standard_normal(L.hv)).astype(np.float32)
+    L.dt_bias = (0.3 * rng.standard_normal(L.hv)).astype(np.float32)
+    pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 4)
+    seqs, refs = [], []
+    for _ in range(4):
+        s = pool.open()
+        m, h = seeded_state(rng, L)
+        pool.write(s, m, h)
+        seqs.append(s)
+        refs.append((m.copy(), h.copy()))
+    for call, rows in enumerate(([64, 45, 1, 9], [32, 100, 33, 1], [17, 1, 64, 31])):
+        run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, f"call {call}")
+    pool.destroy()
+
+
+def test_gdn_chunked_form_key_groups_and_conv_sizes(pkg, backend, rng):
+    # key groups of 1 and 4, conv kernels 1 (no history), 2 and 6
+    for hk, hv, K in ((4, 4, 1), (1, 4, 2), (2, 8, 6)):
+        L = Layer(rng, hk, hv, 128, 128, K)
+        pool = pkg.GdnState(backend, hk, hv, 128, 128, K, 2)
+        s = pool.open()
+        m, h = seeded_state(rng, L)
+        pool.write(s, m, h)
+        run_batch(pkg, backend, pool, L, [s], [70], [(m, h)], rng, f"hk {hk} hv {hv} K {K}")
+        pool.destroy()
+
+
+def test_gdn_chunked_equals_token_serial_and_bf16_device(pkg, backend, rng):
+    # invariant: one 96-row call == the same rows one at a time (decode
+    # kernel), within the f32 tolerance; then bf16 device inputs, async
+    import torch
+    L = Layer(rng, 16, 32)
+    pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 3)
+    a = pool.open()
+    m, h = seeded_state(rng, L)
+    pool.write(a, m, h)
+    b = pool.fork(a)
+    x = L.inputs(rng, 96)
+    whole = plugin_rows(pkg, backend, pool, L, [a], [96], x)
+    serial = np.concatenate([plugin_rows(pkg, backend, pool, L, [b], [1],
+                                         tuple(t[r:r + 1] for t in x)) for r in range(96)])
+    close(whole, serial, what="chunked vs token-serial")
+    close(pool.read(a)[0], pool.read(b)[0], what="state chunked vs token-serial")
+    c = pool.open()
+    m, h = seeded_state(rng, L)
+    pool.write(c, m, h)
+    qkv, z, av, bv = (O.bf16_round(t) for t in L.inputs(rng, 80))
+    exp = oracle_rows(L, (qkv, z, av, bv), m, h)
+    dev = [torch.from_numpy(t).to(torch.bfloat16).cuda() for t in (qkv, z, av, bv)]
+    out = torch.zeros((80, L.hv * L.dv), device="cuda")
+    w = [torch.from_numpy(t).cuda() for t in (L.a_log, L.dt_bias, L.conv, L.norm)]
+    pkg.gdn_forward(backend, pool, [c], [80], *dev, *w, out, eps=1e-6, asynchronous=True)
+    backend.synchronize()
+    close(out.cpu().numpy(), exp, what="bf16 device inputs")
+    close(pool.read(c)[0], m, what="bf16 state")
+    pool.destroy()
