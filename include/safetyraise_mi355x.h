@@ -155,11 +155,14 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_read(
  *          positions [rows][3] int32 (the three MRoPE axes; text uses p,p,p).
  * Output:  out [rows][heads*head_dim] f32.
  * seq_ids and seq_rows are always host arrays.  The kernel is chosen per
- * sequence: fewer than 16 rows go to the split-K decode kernel (row by row),
- * 16 or more to the MFMA prefill kernels.  A synchronous call whose prefill
- * rows meet a K/V/q value beyond the fp16 range (|x| >= 65520) recomputes
- * those sequences on the split-K path; an asynchronous one reports it at the
- * next synchronous call.
+ * sequence: one row goes to the split-K decode kernel; 2..15 rows (MTP
+ * verify drafts) with rows * heads/kv_heads <= 64 and head_dim <= 128 to the
+ * multi-row split-K verify kernel (every cached K/V tile read once for all
+ * rows); 16 or more rows to the MFMA prefill kernels; anything else row by
+ * row on the decode kernel.  A synchronous call whose verify or prefill rows
+ * meet a K/V/q value beyond the fp16 range of the MFMA operands
+ * (|x| >= 65520) recomputes those sequences on the f32 split-K path; an
+ * asynchronous one reports it at the next synchronous call.
  * ---------------------------------------------------------------------- */
 typedef struct safetyraise_kernel_attention_args {
     uint32_t struct_size;
@@ -237,7 +240,12 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_write(
  *   out  = RMSNorm(o per value head, norm, eps, no offset) * silu(z).
  * Inputs: qkv [rows][C], z [rows][Hv*Dv], a and b [rows][Hv] (f32, or bf16
  * with INPUT_BF16); a_log, dt_bias [Hv], conv_weight [C][K], norm [Dv] f32.
- * Output: out [rows][Hv*Dv] f32. */
+ * Output: out [rows][Hv*Dv] f32.
+ * Calls with at most 8 rows per sequence run the recurrence token by token
+ * (one workgroup per sequence and value head, state in registers); longer
+ * calls with value_dim 128 and a 16-byte aligned qkv run the chunked (WY)
+ * form on f32 MFMA in chunks of 32 rows, which equals the token-serial
+ * result within f32 rounding. */
 typedef struct safetyraise_kernel_gdn_args {
     uint32_t struct_size;
     uint32_t flags;
