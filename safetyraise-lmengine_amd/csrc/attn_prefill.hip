@@ -47,6 +47,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -118,6 +119,13 @@ __device__ __forceinline__ float bf16_elem(const u32x4 &w, int e) {
 template <typename T>
 __device__ __forceinline__ void pin(T &x) {
     asm volatile("" : "+v"(x));
+}
+// The same for a wave-uniform value: it must be in scalar registers here, so
+// a kernel-argument load completes at this point (loads issued together
+// complete together) and is not re-issued later at each use.
+template <typename T>
+__device__ __forceinline__ void pin_s(T &x) {
+    asm volatile("" : "+s"(x));
 }
 
 // Sum of the 8 fp16 values of x added to acc in f32 (v_dot2_f32_f16 with 1s).
@@ -411,18 +419,162 @@ struct TileIo {
     }
 };
 
+// The same tile images as TileIo (K rows with k_swz, V^T with vt_swz), but
+// every per-thread offset is recomputed from the thread's index gt at each
+// use instead of being held in registers for the whole kernel (callers pass
+// a freshly pinned copy of gt, so the compiler cannot hoist the offsets).
+template <int D, int NTHR, bool kTilePage>
+struct LeanIo {
+    static constexpr int KCH = D / 8;                    // 16-byte chunks per row
+    static constexpr int KSTEP = NTHR / KCH;             // keys per pass of the threads
+    static constexpr int KL = kKeyTile / KSTEP;          // K chunks per thread
+    static constexpr int VU = (kKeyTile / 4) * KCH;      // (4-key group, chunk) units
+    static constexpr int VL = (VU + NTHR - 1) / NTHR;
+    static_assert(NTHR % KCH == 0 && kKeyTile % KSTEP == 0, "thread layout");
+    const uint16_t *k_pages;
+    const uint16_t *v_pages;
+    const int32_t *table;
+    size_t head_base;
+    uint32_t lpt, pt_mask, n_keys, n_tiles;
+
+    __device__ __forceinline__ void init(const PrefillParams &p, const BlockPos &b) {
+        k_pages = p.k_pages;
+        v_pages = p.v_pages;
+        table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
+        head_base = (size_t)b.kvh * p.num_pages;
+        lpt = p.log2_page_tokens;
+        pt_mask = (1u << lpt) - 1;
+        n_keys = b.n_keys;
+        n_tiles = b.n_tiles;
+    }
+    __device__ __forceinline__ uint32_t page_of(uint32_t t) const {
+        return kTilePage ? (uint32_t)table[(min(t, n_tiles - 1) * kKeyTile) >> lpt] : 0u;
+    }
+    // element offset of tile t's first key in its page (kTilePage; pg = page_of(t))
+    __device__ __forceinline__ size_t tile_base(uint32_t t, uint32_t pg) const {
+        return kTilePage ? (((head_base + pg) << lpt) + ((t * kKeyTile) & pt_mask)) * D : 0;
+    }
+    __device__ __forceinline__ size_t row(uint32_t t, size_t base, uint32_t key) const {
+        if constexpr (kTilePage) {
+            return base + (size_t)key * D;
+        } else {
+            const uint32_t tok = min(t * kKeyTile + key, n_keys - 1);
+            return (((head_base + (uint32_t)table[tok >> lpt]) << lpt) + (tok & pt_mask)) * D;
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void load_k(u32x4 (&r)[N], uint32_t t, size_t base, uint32_t gt) const {
+        static_assert(N >= KL, "staging registers");
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) r[i] = *(const u32x4 *)(k_pages + row(t, base, k0 + i * KSTEP) + ch * 8);
+    }
+    template <int N>
+    __device__ __forceinline__ void load_v(u32x4 (&r)[N], uint32_t t, size_t base, uint32_t gt) const {
+        static_assert(N >= 4 * VL, "staging registers");
+        const uint32_t ch = gt % KCH;
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            const uint32_t u = min(gt + i * NTHR, (uint32_t)VU - 1);  // (threads past VU repeat a unit)
+            const uint32_t g = u / KCH;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[4 * i + j] = *(const u32x4 *)(v_pages + row(t, base, 4 * g + j) + ch * 8);
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void store_k(const u32x4 (&r)[N], unsigned char *kt, uint32_t gt) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const uint32_t key = k0 + i * KSTEP;
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(r[i][j]), bf16hi(r[i][j]));
+            *(u32x4 *)(kt + key * (D * 2) + ((ch ^ k_swz<D>(key)) * 16)) = f;
+        }
+    }
+    // valid_keys: keys of the tile that exist; V rows past them become 0
+    template <int N>
+    __device__ __forceinline__ void store_v(const u32x4 (&r)[N], unsigned char *vt, uint32_t valid_keys,
+                                            uint32_t gt) const {
+        const uint32_t ch = gt % KCH;
+#pragma unroll
+        for (int i = 0; i < VL; ++i) {
+            const uint32_t u = gt + i * NTHR;
+            if ((VL * NTHR != VU) && u >= (uint32_t)VU) continue;
+            const uint32_t g = u / KCH;
+            u32x4 w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) w[j] = (4 * g + j < valid_keys) ? r[4 * i + j] : u32x4{0, 0, 0, 0};
+            const uint32_t unit = 2 * (g >> 2) + (g & 1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = ch * 8 + e;
+                const uint32_t lo = pack_f16x2(bf16_elem(w[0], e), bf16_elem(w[1], e));
+                const uint32_t hi = pack_f16x2(bf16_elem(w[2], e), bf16_elem(w[3], e));
+                *(uint2 *)(vt + d * (kKeyTile * 2) + ((unit ^ vt_swz(d)) * 16) + 8 * ((g & 3) >> 1)) =
+                    make_uint2(lo, hi);
+            }
+        }
+    }
+};
+
 // One wave's query rows: q RMSNorm (math.rs:28-50), RoPE with the row's
 // cos/sin from the append kernel, scale by log2(e)/sqrt(D), fp16.  The lane
 // holds row (row0 + col) and dims 16s + 8h + j (the B operand of S^T).
+// Scalar inputs of q_operands, read from the kernel arguments once at kernel
+// entry (q_args), so the prologue does not wait for one argument load after
+// another.
+struct QArgs {
+    const void *q;
+    const float *q_norm;
+    const float2 *rope_cs;
+    uint32_t *err_word;
+    uint32_t flags;
+    uint32_t rotary_dim;
+    float eps;
+};
+
+__device__ __forceinline__ QArgs q_args(const PrefillParams &p) {
+    QArgs a{p.q, p.q_norm, p.rope_cs, p.err_word, p.flags, p.rotary_dim, p.eps};
+    pin_s(a.q);
+    pin_s(a.q_norm);
+    pin_s(a.rope_cs);
+    pin_s(a.err_word);
+    pin_s(a.flags);
+    pin_s(a.rotary_dim);
+    pin_s(a.eps);
+    return a;
+}
+
 template <int D>
-__device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase, uint32_t call_row,
+__device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_t call_row,
                                            int h, int lane, f16x8 (&qop)[D / 16]) {
     constexpr int NS = D / 16;
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
-    // (one branch around all loads of a format, so that they are in flight
-    // together)
+    // Every global input is requested before any is used, so that the
+    // prologue waits for one round trip: the norm weights (q_norm is always
+    // readable: the host passes a zero buffer when there is no QK-norm), the
+    // row's RoPE (cos, sin) pairs (the host routes only rotary_dim >= 32, a
+    // multiple of 32, here) and q itself.
+    const uint32_t half = p.rotary_dim / 2;
+    const uint32_t hsteps = p.rotary_dim / 32;
+    const float2 *cs_row = p.rope_cs + (size_t)call_row * half;
+    f32x4 gw[NS][2];
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        gw[st][0] = *(const f32x4 *)(p.q_norm + 16 * st + 8 * h);
+        gw[st][1] = *(const f32x4 *)(p.q_norm + 16 * st + 8 * h + 4);
+    }
+    f32x4 csv[NS / 2][4];
+#pragma unroll
+    for (int st = 0; st < NS / 2; ++st) {
+        const f32x4 *c4 = (const f32x4 *)(cs_row + 16 * min((uint32_t)st, hsteps - 1) + 8 * h);
+#pragma unroll
+        for (int j2 = 0; j2 < 4; ++j2) csv[st][j2] = c4[j2];  // (cos, sin) of pairs 2 j2, 2 j2 + 1
+    }
     float x[NS][8];
     if (bf16_in) {
 #pragma unroll
@@ -455,20 +607,32 @@ __device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase,
         const float inv = 1.0f / sqrtf(variance + p.eps);
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const float4 wa = *(const float4 *)(p.q_norm + 16 * st + 8 * h);
-            const float4 wb = *(const float4 *)(p.q_norm + 16 * st + 8 * h + 4);
-            const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[st][j] = x[st][j] * inv * (wv[j] + norm_add);
+            for (int j = 0; j < 8; ++j) x[st][j] = x[st][j] * inv * (gw[st][j >> 2][j & 3] + norm_add);
         }
     }
-    // pairs (i, i + rotary_dim/2); the host routes only rotary_dim/2 that is
-    // a multiple of 16 here, so both halves of a pair sit in this lane (the
-    // partner step st + hsteps is selected with compile-time indices so that
-    // x stays in registers)
-    const uint32_t half = p.rotary_dim / 2;
-    const uint32_t hsteps = p.rotary_dim / 32;
-    const float2 *cs_row = p.rope_cs + (size_t)call_row * half;
+    // pairs (i, i + rotary_dim/2): both halves of a pair sit in this lane
+    // (the partner step st + hsteps is selected with compile-time indices so
+    // that x stays in registers; full rotary, the common case, has its own
+    // straight-line copy)
+    if (hsteps == (uint32_t)(NS / 2)) {
+#pragma unroll
+        for (int st = 0; st < NS / 2; ++st) {
+#pragma unroll
+            for (int j2 = 0; j2 < 4; ++j2) {
+                const f32x4 cc = csv[st][j2];
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int j = 2 * j2 + k;
+                    const float cs = k ? cc.z : cc.x;
+                    const float sn = k ? cc.w : cc.y;
+                    const float left = x[st][j], right = x[st + NS / 2][j];
+                    x[st][j] = left * cs - right * sn;
+                    x[st + NS / 2][j] = right * cs + left * sn;
+                }
+            }
+        }
+    } else {
 #pragma unroll
     for (int st = 0; st < NS / 2; ++st) {
         if ((uint32_t)st < hsteps) {
@@ -480,10 +644,9 @@ __device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase,
                     for (int j = 0; j < 8; ++j) right[j] = x[st + k][j];
                 }
             }
-            const float4 *c4 = (const float4 *)(cs_row + 16 * st + 8 * h);
 #pragma unroll
             for (int j2 = 0; j2 < 4; ++j2) {
-                const float4 cc = c4[j2];  // (cos, sin) of pairs 2*j2 and 2*j2 + 1
+                const f32x4 cc = csv[st][j2];
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const int j = 2 * j2 + k;
@@ -502,6 +665,7 @@ __device__ __forceinline__ void q_operands(const PrefillParams &p, size_t qbase,
                 }
             }
         }
+    }
     }
     const float qscale = (1.0f / sqrtf((float)D)) * kLog2e;
 #pragma unroll
@@ -674,6 +838,7 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
     const int lane = tid & 63;
     const int h = lane >> 5;
     const int col = lane & 31;
+    const QArgs qa = q_args(p);
     const BlockPos b = block_pos(p, kRowTile * R);
     if (!b.active) return;
     const uint32_t head = b.kvh * G + (wave % G);
@@ -695,7 +860,7 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
         io.load_v(vreg, 0, pg0);
     }
     f16x8 qop[NS];
-    q_operands<D>(p, qbase, b.m.row0 + my_row, h, lane, qop);
+    q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
 
     f32x16 oacc[NT];
 #pragma unroll
@@ -756,7 +921,7 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     constexpr int RG = 4 / G;  // row blocks per group
     constexpr int NS = D / 16;
     constexpr int NT = D / 32;
-    using Io = TileIo<D, 256, kTilePage>;
+    using Io = LeanIo<D, 256, kTilePage>;
     constexpr int SL = (Io::KL > 4 * Io::VL) ? Io::KL : 4 * Io::VL;
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char *kbuf = lds;                         // 2 K tiles
@@ -769,6 +934,7 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     const int col = lane & 31;
     const int grp = wave >> 2;  // waves w and w + 4 share a SIMD
     const int gw = wave & 3;
+    const QArgs qa = q_args(p);
     const BlockPos b = block_pos(p, 2 * kRowTile * RG);
     if (!b.active) return;
     const uint32_t head = b.kvh * G + (gw % G);
@@ -781,24 +947,30 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     const uint32_t n = b.n_tiles;
 
     Io io;
-    io.init(tid & 255, p, b);
-    u32x4 stage[SL];
+    io.init(p, b);
+    const uint32_t gt0 = tid & 255;
+    // staging registers, two sets: tile j's data lives in stage[j & 1], so a
+    // load never waits for the LDS stores that read the other set
+    u32x4 stage0[SL] = {}, stage1[SL] = {};
     // tile 0: K by group 0, V by group 1; then each group's tile 1 in flight
+    // tiles 0 and 1 (K by group 0, V by group 1) and tile 2's page id are
+    // requested before the q prologue, so their latency overlaps it
     {
-        const uint32_t pg0 = io.page_of(0);
-        if (grp == 0) io.load_k(stage, 0, pg0);
-        else io.load_v(stage, 0, pg0);
+        const uint32_t pg0 = io.page_of(0), pg1 = io.page_of(1);
+        const size_t tb0 = io.tile_base(0, pg0), tb1 = io.tile_base(min(1u, n - 1), pg1);
+        if (grp == 0) {
+            io.load_k(stage0, 0, tb0, gt0);
+            io.load_k(stage1, min(1u, n - 1), tb1, gt0);
+        } else {
+            io.load_v(stage0, 0, tb0, gt0);
+            io.load_v(stage1, min(1u, n - 1), tb1, gt0);
+        }
     }
-    f16x8 qop[NS];
-    q_operands<D>(p, qbase, b.m.row0 + my_row, h, lane, qop);
-    if (grp == 0) io.store_k(stage, kbuf);
-    else io.store_v(stage, vbuf, b.n_keys);
     uint32_t pg_next = io.page_of(2);
-    if (n > 1) {
-        const uint32_t pg1 = io.page_of(1);
-        if (grp == 0) io.load_k(stage, 1, pg1);
-        else io.load_v(stage, 1, pg1);
-    }
+    f16x8 qop[NS];
+    q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
+    if (grp == 0) io.store_k(stage0, kbuf, gt0);
+    else io.store_v(stage0, vbuf, b.n_keys, gt0);
     f32x16 oacc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
@@ -808,24 +980,32 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     __syncthreads();
     if (grp == 1) __syncthreads();  // group 1 starts one phase later
 
-    for (uint32_t t = 0; t < n; ++t) {
+    // one iteration for tile t: `cur` holds tile t+1 (stored now), `nxt`
+    // receives tile t+2
+    auto step = [&](uint32_t t, u32x4 (&cur)[SL], u32x4 (&nxt)[SL]) __attribute__((always_inline)) {
         // ---- M phase: PV(t-1), S(t) ----
         if (t > 0) pv_tile<D>(vbuf + ((t - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
         f32x16 sacc[2];
         s_tile<D>(kbuf + (t & 1) * kTileBytes<D>, qop, h, col, sacc);
         __syncthreads();
         // ---- V phase: softmax(t), stage the group's tile t+1, load t+2 ----
+        // The page id of tile t+2 (requested one phase earlier) is consumed
+        // here, before this phase's LDS stores are issued, so that its wait
+        // does not also wait for them.  Then tile t+3's is requested.
+        size_t tb_next = io.tile_base(t + 2, pg_next);
+        pin(tb_next);
+        pg_next = io.page_of(t + 3);
         const uint32_t key0 = t * kKeyTile;
         softmax_tile<D>(sacc, key0, key0 + kKeyTile - 1 > first_row_limit, key_limit, h, m_run,
                         l_run, oacc, pop);
+        uint32_t gt = gt0;
+        pin(gt);
         if (t + 1 < n) {
-            if (grp == 0) io.store_k(stage, kbuf + ((t + 1) & 1) * kTileBytes<D>);
-            else io.store_v(stage, vbuf + ((t + 1) % 3) * kTileBytes<D>, b.n_keys - key0 - kKeyTile);
+            if (grp == 0) io.store_k(cur, kbuf + ((t + 1) & 1) * kTileBytes<D>, gt);
+            else io.store_v(cur, vbuf + ((t + 1) % 3) * kTileBytes<D>, b.n_keys - key0 - kKeyTile, gt);
             if (t + 2 < n) {
-                const uint32_t pg = pg_next;
-                pg_next = io.page_of(t + 3);
-                if (grp == 0) io.load_k(stage, t + 2, pg);
-                else io.load_v(stage, t + 2, pg);
+                if (grp == 0) io.load_k(nxt, t + 2, tb_next, gt);
+                else io.load_v(nxt, t + 2, tb_next, gt);
             }
         }
         // the softmax results stay in this phase
@@ -834,6 +1014,10 @@ attn_prefill_pp_kernel(const PrefillParams p) {
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt) pin(oacc[tt]);
         __syncthreads();
+    };
+    for (uint32_t t = 0; t < n; t += 2) {
+        step(t, stage1, stage0);
+        if (t + 1 < n) step(t + 1, stage0, stage1);
     }
     pv_tile<D>(vbuf + ((n - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
     if (grp == 0) __syncthreads();  // matches group 1's extra barrier
@@ -844,7 +1028,7 @@ attn_prefill_pp_kernel(const PrefillParams p) {
 }
 
 template <int D, int G>
-constexpr bool kUsePingPong = (D <= 128) && (G == 1 || G == 2 || G == 4);
+constexpr bool kUsePingPong = (D == 128) && (G == 1 || G == 2 || G == 4);
 
 template <int D, int G>
 uint32_t rows_per_block_dg() {
@@ -1043,6 +1227,7 @@ attn_verify_kernel(const VerifyParams vp) {
     const uint32_t j = blockIdx.x / p.kv_heads;
     uint32_t s = 0;
     while (s + 1 < p.nseq && vp.blk0[s + 1] <= j) ++s;
+    const QArgs qa = q_args(p);
     const PrefillMeta m = p.meta[s];
     const uint32_t part = j - vp.blk0[s];
     const uint32_t total = m.ctx + m.rows;
@@ -1123,7 +1308,7 @@ attn_verify_kernel(const VerifyParams vp) {
     const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
     const size_t qbase = (size_t)(m.row0 + r) * p.heads * hs + (size_t)head * hs;
     f16x8 qop[NS];
-    if (computes) q_operands<D>(p, qbase, m.row0 + r, h, lane, qop);
+    if (computes) q_operands<D>(qa, qbase, m.row0 + r, h, lane, qop);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_barrier();  // (A)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
@@ -1277,8 +1462,10 @@ PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
     p.q = a.q;
     p.k = a.k;
     p.v = a.v;
-    p.q_norm = a.q_norm;
-    p.k_norm = a.k_norm;
+    // without QK-norm the kernels still read a norm vector (unused): the
+    // context's zeroed error-word block is readable and large enough
+    p.q_norm = a.q_norm != nullptr ? a.q_norm : (const float *)a.err_word;
+    p.k_norm = a.k_norm != nullptr ? a.k_norm : (const float *)a.err_word;
     p.positions = a.positions;
     p.out = a.out;
     p.rope_cs = (float2 *)rope_scratch;
@@ -1304,7 +1491,7 @@ PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
 bool prefill_supported(const AttnLaunch &a) {
     const uint32_t g = a.heads / a.kv_heads;
     return (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) && g >= 1 && g <= 8 &&
-           a.rotary_dim % 32 == 0;
+           a.rotary_dim >= 32 && a.rotary_dim % 32 == 0;
 }
 
 size_t prefill_rope_bytes(const AttnLaunch &a, uint64_t total_rows) {

@@ -151,10 +151,13 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_create_context(
     }
     if (err == hipSuccess) {
         ctx->stream = ctx->own_stream;
-        err = hipMalloc(&ctx->d_error_word, 256);
+        // word 0 is the error word; the rest stays zero and serves the
+        // prefill kernels as a readable stand-in for absent norm weights
+        // (up to 256 floats)
+        err = hipMalloc(&ctx->d_error_word, kErrorBlockBytes);
     }
     if (err == hipSuccess) {
-        err = hipMemset(ctx->d_error_word, 0, 256);
+        err = hipMemset(ctx->d_error_word, 0, kErrorBlockBytes);
     }
     if (err != hipSuccess) {
         if (ctx->d_error_word != nullptr) (void)hipFree(ctx->d_error_word);

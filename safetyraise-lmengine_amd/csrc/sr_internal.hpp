@@ -24,6 +24,7 @@ constexpr int32_t kAbiMismatch = SAFETYRAISE_KERNEL_STATUS_ABI_MISMATCH;
 // Bits of the context's sticky device error word (set by kernels).
 constexpr uint32_t kErrNonFiniteKv = 1u;        // PagedKvCache::append rejects (state.rs:56-58)
 constexpr uint32_t kErrNonFiniteVariance = 2u;  // rms_norm rejects (math.rs:39-41)
+constexpr size_t kErrorBlockBytes = 1024;  // error word + zero block (>= 256 floats)
 // A prefill row's output is not finite: some K, V or q value is outside the fp16
 // operand range of the MFMA prefill kernel; synchronous calls recompute on the
 // f32 split-K path.
