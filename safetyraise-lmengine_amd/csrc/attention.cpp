@@ -55,10 +55,13 @@ int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta
     return kOk;
 }
 
-int32_t run_verify_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
+// The first pack launched carries the call's inline page-table entries
+// (AttnLaunch::tbl_*); they are cleared once a launch has taken them.
+int32_t run_verify_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack) {
     DecodePlanInput plan{ctx->num_cus, reserve_partials, ctx};
     const hipError_t e = launch_attn_verify(ctx->stream, a, pack.data(), (int)pack.size(),
                                             ctx->rope_scratch.ptr, plan);
+    a.tbl_n = 0;
     if (e != hipSuccess) {
         if (ctx->error.empty() || e != hipErrorOutOfMemory) {
             return hip_fail(ctx, e, "verify attention launch");
@@ -68,9 +71,10 @@ int32_t run_verify_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta
     return kOk;
 }
 
-int32_t run_prefill_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
+int32_t run_prefill_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack) {
     const hipError_t e =
         launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size(), ctx->rope_scratch.ptr);
+    a.tbl_n = 0;
     if (e != hipSuccess) return hip_fail(ctx, e, "prefill attention launch");
     return kOk;
 }
@@ -202,17 +206,33 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         L.out = (float *)(base + out_off);
     }
 
+    // Routing (below): 16+ rows -> prefill, 2..15 supported rows -> verify,
+    // the rest -> row-serial decode.  When no row takes the decode path, the
+    // call's page-table entries (if few) travel in the first append kernel's
+    // arguments instead of a separate update launch.
+    const bool prefill_ok = prefill_supported(L);
+    bool any_serial_route = false;
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        const uint32_t r = A.seq_rows[i];
+        const bool fast = (r >= kPrefillMinRows && prefill_ok) ||
+                          (r < kPrefillMinRows && verify_supported(L, r));
+        any_serial_route = any_serial_route || !fast;
+    }
     std::vector<uint64_t> old_len(A.num_seqs);
-    {
-        TableBatch batch;  // one page-table upload for the whole call
-        for (uint32_t i = 0; i < A.num_seqs; ++i) {
-            old_len[i] = pool->seqs[A.seq_ids[i]].len;
-            int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i], &batch);
-            if (st != kOk) {
-                kv_flush_table(ctx, pool, batch);
-                return st;
-            }
+    TableBatch batch;  // one page-table upload for the whole call
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        old_len[i] = pool->seqs[A.seq_ids[i]].len;
+        int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i], &batch);
+        if (st != kOk) {
+            kv_flush_table(ctx, pool, batch);
+            return st;
         }
+    }
+    if (!any_serial_route && batch.idx.size() <= kInlineTable) {
+        L.tbl_idx = batch.idx.data();
+        L.tbl_val = batch.val.data();
+        L.tbl_n = (uint32_t)batch.idx.size();
+    } else {
         int32_t st = kv_flush_table(ctx, pool, batch);
         if (st != kOk) return st;
     }
@@ -223,7 +243,6 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     std::vector<uint8_t> serial(A.num_seqs, 1);
     uint32_t serial_rows = 0;
     bool any_prefill = false;
-    const bool prefill_ok = prefill_supported(L);
     if (prefill_ok) {
         int32_t st = ensure_buffer(ctx, ctx->rope_scratch, prefill_rope_bytes(L, total_rows), false);
         if (st != kOk) return st;

@@ -8,8 +8,10 @@
 // context plus rows 0..i (math.rs:102-155), and the Qwen3.5 output gate.
 //
 // Two kernels per launch:
-//   kv_append_rows_kernel  one workgroup per new row: the row's RoPE cos/sin
-//                          (once per rotary pair, also saved for the q side),
+//   kv_append_rows_kernel  one wave per new row (four per workgroup): the
+//                          row's RoPE cos/sin (once per rotary pair, also
+//                          saved for the q side), the call's page-table
+//                          entries when they travel in the arguments,
 //                          K RMSNorm + RoPE and V of every KV head, rounded
 //                          to bf16 into the pages (the reference appends
 //                          before it attends, so every row's keys must be in
@@ -89,6 +91,10 @@ struct PrefillParams {
     uint32_t max_blk;
     RopeTable rope;
     PrefillMeta meta[kMetaPerLaunch];
+    // page-table entries the append kernel writes (and uses for its own rows)
+    uint32_t tbl_n;
+    uint32_t tbl_idx[kInlineTable];
+    int32_t tbl_val[kInlineTable];
 };
 
 // Max / sum of x over lanes l and l^32 (both halves get the same bits).
@@ -144,13 +150,23 @@ __device__ __forceinline__ float sum_f16x8(const f16x8 &x, float acc) {
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams p) {
     constexpr int EPL = D / 64;
-    __shared__ float cs_s[128];
-    __shared__ float sn_s[128];
+    constexpr int kHeadBatch = 8;  // KV heads whose loads are in flight together
+    __shared__ float cs_s[4][128];
+    __shared__ float sn_s[4][128];
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
     const PrefillMeta m = p.meta[blockIdx.y];
-    const uint32_t r = blockIdx.x;
+    // entries of this call's page-table update: block (0,0) writes them for
+    // the kernels that follow; every row takes its own page from the list
+    // (the table itself may not hold it yet)
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        for (uint32_t i = tid; i < p.tbl_n; i += 256) {
+            ((int32_t *)p.page_table)[p.tbl_idx[i]] = p.tbl_val[i];
+        }
+    }
+    // one wave per row; no barrier below, so a wave past the rows just ends
+    const uint32_t r = blockIdx.x * 4 + wave;
     if (r >= m.rows) return;
     const uint32_t row = m.row0 + r;
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
@@ -158,74 +174,94 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     const bool interleaved = (p.flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
 
-    // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with an IEEE
-    // f32 division (math.rs:90-91); once per row, shared with the q side
-    const uint32_t half = p.rotary_dim / 2;
-    if ((uint32_t)tid < half) {
-        const int32_t *pos3 = p.positions + (size_t)row * 3;
-        const int axis = rope_axis(tid, p.mrope, interleaved);
-        const float angle = (float)pos3[axis] / p.rope.denom[tid];
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        cs_s[tid] = cs;
-        sn_s[tid] = sn;
-        p.rope_cs[(size_t)row * half + tid] = make_float2(cs, sn);
-    }
-    __syncthreads();
-
     const uint32_t tok = m.ctx + r;
-    const int32_t page = p.page_table[(size_t)m.slot * p.pages_per_seq + (tok >> p.log2_page_tokens)];
+    const uint32_t tidx = m.slot * p.pages_per_seq + (tok >> p.log2_page_tokens);
+    int32_t page = p.page_table[tidx];
+    {
+        const bool hit = (uint32_t)lane < p.tbl_n && p.tbl_idx[min((uint32_t)lane, kInlineTable - 1)] == tidx;
+        const uint64_t mask = __builtin_amdgcn_ballot_w64(hit);
+        if (mask != 0) page = p.tbl_val[__builtin_ctzll(mask)];
+    }
     const uint32_t pt_mask = (1u << p.log2_page_tokens) - 1;
+    const uint32_t half = p.rotary_dim / 2;
+
     bool finite = true;
-    for (uint32_t kvh = wave; kvh < p.kv_heads; kvh += 4) {
-        const size_t src = ((size_t)row * p.kv_heads + kvh) * D;
-        float x[EPL], vv[EPL];
+    for (uint32_t kb = 0; kb < p.kv_heads; kb += kHeadBatch) {
+        // every load of the batch first (heads past kv_heads repeat the last)
+        float x[kHeadBatch][EPL], vv[kHeadBatch][EPL], wk[EPL];
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            x[i] = load_act(p.k, src + lane + 64 * i, bf16_in);
-            vv[i] = load_act(p.v, src + lane + 64 * i, bf16_in);
-        }
-        if (qk_norm) {
-            // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
-            float ss = 0.0f;
+        for (int hh = 0; hh < kHeadBatch; ++hh) {
+            const uint32_t kvh = min(kb + hh, p.kv_heads - 1);
+            const size_t src = ((size_t)row * p.kv_heads + kvh) * D;
 #pragma unroll
-            for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
-            ss = sum64(ss);
-            const float variance = ss / (float)D;
-            if (!isfinite(variance) && lane == 0) {
-                atomicOr(p.err_word, kErrNonFiniteVariance);
-            }
-            const float inv = 1.0f / sqrtf(variance + p.eps);
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (p.k_norm[lane + 64 * i] + norm_add);
-        }
-        // rotate-half over the first rotary_dim dims (math.rs:52-99): dim e
-        // pairs with e +- half, which lives in lane (e +- half) % 64
-        float y[EPL];
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            const uint32_t e = lane + 64 * i;
-            y[i] = x[i];
-            const uint32_t pe = e < half ? e + half : e - half;
-            float partner = 0.0f;
-#pragma unroll
-            for (int j = 0; j < EPL; ++j) {
-                const float t = __shfl(x[j], (int)(pe & 63));
-                if ((int)(pe >> 6) == j) partner = t;
-            }
-            if (e < p.rotary_dim) {
-                const uint32_t pi = e < half ? e : e - half;
-                y[i] = e < half ? x[i] * cs_s[pi] - partner * sn_s[pi]
-                                : x[i] * cs_s[pi] + partner * sn_s[pi];
+            for (int i = 0; i < EPL; ++i) {
+                x[hh][i] = load_act_nb(p.k, src + lane + 64 * i, bf16_in);
+                vv[hh][i] = load_act_nb(p.v, src + lane + 64 * i, bf16_in);
             }
         }
-        const size_t dst =
-            ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D;
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) {
-            finite = finite && isfinite(y[i]) && isfinite(vv[i]);
-            p.k_pages[dst + lane + 64 * i] = f32_to_bf16(y[i]);
-            p.v_pages[dst + lane + 64 * i] = f32_to_bf16(vv[i]);
+        for (int i = 0; i < EPL; ++i) wk[i] = p.k_norm[lane + 64 * i];  // readable without QK-norm too
+        if (kb == 0) {
+            // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with
+            // an IEEE f32 division (math.rs:90-91); once per row, shared with
+            // the q side (computed while the loads above are in flight)
+            const int32_t *pos3 = p.positions + (size_t)row * 3;
+            for (uint32_t i = lane; i < half; i += 64) {
+                const int axis = rope_axis(i, p.mrope, interleaved);
+                const float angle = (float)pos3[axis] / p.rope.denom[i];
+                float sn, cs;
+                sincosf(angle, &sn, &cs);
+                cs_s[wave][i] = cs;
+                sn_s[wave][i] = sn;
+                p.rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < kHeadBatch; ++hh) {
+            const uint32_t kvh = kb + hh;
+            if (kvh >= p.kv_heads) break;  // wave-uniform
+            if (qk_norm) {
+                // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) ss += x[hh][i] * x[hh][i];
+                ss = sum64(ss);
+                const float variance = ss / (float)D;
+                if (!isfinite(variance) && lane == 0) {
+                    atomicOr(p.err_word, kErrNonFiniteVariance);
+                }
+                const float inv = 1.0f / sqrtf(variance + p.eps);
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) x[hh][i] = x[hh][i] * inv * (wk[i] + norm_add);
+            }
+            // rotate-half over the first rotary_dim dims (math.rs:52-99): dim
+            // e pairs with e +- half, which lives in lane (e +- half) % 64
+            float y[EPL];
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) {
+                const uint32_t e = lane + 64 * i;
+                y[i] = x[hh][i];
+                const uint32_t pe = e < half ? e + half : e - half;
+                float partner = 0.0f;
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) {
+                    const float t = __shfl(x[hh][j], (int)(pe & 63));
+                    if ((int)(pe >> 6) == j) partner = t;
+                }
+                if (e < p.rotary_dim) {
+                    const uint32_t pi = e < half ? e : e - half;
+                    y[i] = e < half ? x[hh][i] * cs_s[wave][pi] - partner * sn_s[wave][pi]
+                                    : x[hh][i] * cs_s[wave][pi] + partner * sn_s[wave][pi];
+                }
+            }
+            const size_t dst =
+                ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) {
+                finite = finite && isfinite(y[i]) && isfinite(vv[hh][i]);
+                p.k_pages[dst + lane + 64 * i] = f32_to_bf16(y[i]);
+                p.v_pages[dst + lane + 64 * i] = f32_to_bf16(vv[hh][i]);
+            }
         }
     }
     if (!finite) atomicOr(p.err_word, kErrNonFiniteKv);
@@ -1079,7 +1115,7 @@ hipError_t launch_dg(hipStream_t stream, PrefillParams &p, const SeqMeta *seqs, 
         max_rows = std::max(max_rows, m.rows);
     }
     p.max_blk = max_blk;
-    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3(max_rows, p.nseq), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3((max_rows + 3) / 4, p.nseq), dim3(256), 0, stream, p);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t blocks = p.max_blk * p.nseq * p.kv_heads;
@@ -1123,6 +1159,8 @@ struct VerifyParams {
     uint32_t blk0[kMetaPerLaunch];  // first partition of each sequence (prefix)
     uint32_t rec0[kMetaPerLaunch];  // first record of each sequence
 };
+static_assert(sizeof(VerifyParams) <= 4096, "kernel arguments stay within 4 KiB");
+
 
 template <int D>
 constexpr int kRecordStride = D + 4;  // m, l, 2 unused, o[D] (16-byte aligned)
@@ -1483,6 +1521,11 @@ PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
     p.eps = a.eps;
     p.nseq = (uint32_t)nseq;
     p.rope = *a.rope;
+    p.tbl_n = a.tbl_n;
+    for (uint32_t i = 0; i < a.tbl_n; ++i) {
+        p.tbl_idx[i] = a.tbl_idx[i];
+        p.tbl_val[i] = a.tbl_val[i];
+    }
     return p;
 }
 
@@ -1564,7 +1607,7 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
     if (vp.partials == nullptr) return hipErrorOutOfMemory;
     // K/V of the new rows and their RoPE cos/sin first (append kernel)
     hipLaunchKernelGGL(a.head_dim == 64 ? kv_append_rows_kernel<64> : kv_append_rows_kernel<128>,
-                       dim3(max_rows, p.nseq), dim3(256), 0, stream, p);
+                       dim3((max_rows + 3) / 4, p.nseq), dim3(256), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t grid = blocks * a.kv_heads;

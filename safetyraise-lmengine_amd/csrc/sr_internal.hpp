@@ -179,7 +179,14 @@ struct AttnLaunch {
     float *out;
     uint32_t *err_word;
     const RopeTable *rope;
+    // page-table entries of this call not yet on the device (at most
+    // kInlineTable): the first append kernel of the call writes them, and
+    // resolves its own rows' pages from them
+    const uint32_t *tbl_idx = nullptr;
+    const int32_t *tbl_val = nullptr;
+    uint32_t tbl_n = 0;
 };
+constexpr uint32_t kInlineTable = 64;
 
 // Host inputs of the decode launch plan: the CU count and a way to get the
 // scratch for per-segment (max, sum, output) records (context-owned, grown
