@@ -69,9 +69,10 @@ def bench_decode(args, torch, pkg):
     rng = np.random.default_rng(args.seed)
     lengths = rng.integers(1024, 32768, size=nseq, endpoint=True)
     total_steps = args.warmup + args.steps
-    max_tokens = int(lengths.max()) + total_steps + 1
+    event_steps = total_steps + args.steps  # a second pass times each call
+    max_tokens = int(lengths.max()) + event_steps + 1
     page = 64
-    pages = int(sum((L + total_steps + page) // page + 1 for L in lengths)) + 8
+    pages = int(sum((L + event_steps + page) // page + 1 for L in lengths)) + 8
 
     backend = pkg.NativeBackend.load()
     stream = torch.cuda.Stream()  # default priority
@@ -102,7 +103,7 @@ def bench_decode(args, torch, pkg):
     v = torch.randn((layers, nseq, kvh * dim), generator=gen, device="cuda")
     out = torch.empty((layers, nseq, heads * dim), device="cuda")
     base = torch.from_numpy(lengths.astype(np.int32)).cuda()
-    positions = [(base + s).view(nseq, 1).repeat(1, 3).contiguous() for s in range(total_steps)]
+    positions = [(base + s).view(nseq, 1).repeat(1, 3).contiguous() for s in range(event_steps)]
 
     P = pkg.plugin
     flags = (P.DEVICE_POINTERS | P.ASYNC | P.QK_NORM | P.MROPE_INTERLEAVED)
@@ -125,7 +126,7 @@ def bench_decode(args, torch, pkg):
         a.kv = pools[layer].handle
         return a
 
-    all_args = [[make_args(s, l) for l in range(layers)] for s in range(total_steps)]
+    all_args = [[make_args(s, l) for l in range(layers)] for s in range(event_steps)]
     fwd = backend.lib.safetyraise_kernel_attention_forward
     ctx = backend.context
 
@@ -147,8 +148,20 @@ def bench_decode(args, torch, pkg):
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0.record(stream)
-    i = 0
     for s in range(args.warmup, total_steps):
+        for l in range(layers):
+            st = fwd(ctx, C.byref(all_args[s][l]))
+            if st != 0:
+                backend.check(st, "attention_forward")
+    t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    # per-call durations in a second pass of the same number of steps (event
+    # markers between calls stall the queue, so they stay out of the timed
+    # region); each call there sees `steps` more keys per sequence
+    i = 0
+    for s in range(total_steps, event_steps):
         for l in range(layers):
             ev[i][0].record(stream)
             st = fwd(ctx, C.byref(all_args[s][l]))
@@ -156,15 +169,13 @@ def bench_decode(args, torch, pkg):
             i += 1
             if st != 0:
                 backend.check(st, "attention_forward")
-    t1.record(stream)
     torch.cuda.synchronize()
     backend.synchronize()
-    total_ms = t0.elapsed_time(t1)
     ms_per_step = total_ms / args.steps
     bytes_total = sum(step_bytes(s) for s in range(args.warmup, total_steps)) * layers
     value = bytes_total / (total_ms * 1e-3) / 1e9
     launch_us = np.array([a.elapsed_time(b) * 1e3 for a, b in ev])
-    per_launch_bytes = bytes_total / len(ev)
+    per_launch_bytes = sum(step_bytes(s) for s in range(total_steps, event_steps)) / args.steps
     achieved = per_launch_bytes / (launch_us.mean() * 1e-6) / 1e9
 
     cpu = None
@@ -340,11 +351,20 @@ def bench_prefill(args, torch, pkg, steps, warmup):
     torch.cuda.synchronize()
     t0.record(stream)
     for s in range(steps):
-        run_step(ev[s])
+        run_step()
     t1.record(stream)
     torch.cuda.synchronize()
     backend.synchronize()
     total_ms = t0.elapsed_time(t1)
+    # per-call durations (the roofline's launch figure) come from a second
+    # pass: event markers between calls stall the queue for a few us each, so
+    # they stay out of the timed region; one unrecorded step queued first
+    # brings the GPU back from idle
+    run_step()
+    for s in range(steps):
+        run_step(ev[s])
+    torch.cuda.synchronize()
+    backend.synchronize()
     ms_per_step = total_ms / steps
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
     per_chunk_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev]).mean(0)
@@ -504,8 +524,15 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
     torch.cuda.synchronize()
     t0.record(stream)
     for s in range(steps):
-        run(warmup + s, ev[s])
+        run(warmup + s)
     t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    # per-call durations in a second pass, outside the timed region, after
+    # one unrecorded step
+    run(warmup + steps)
+    for s in range(steps):
+        run(warmup + steps + 1 + s, ev[s])
     torch.cuda.synchronize()
     backend.synchronize()
     C_ = 2 * hk * dk + hv * dv
@@ -611,10 +638,18 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         t1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0.record(stream)
-        run(ev[s])
+        run()
         t1.record(stream)
         torch.cuda.synchronize()
         total_ms += t0.elapsed_time(t1)
+    backend.synchronize()
+    # per-call durations in a second pass, outside the timed region (event
+    # markers between calls stall the queue)
+    for s in range(steps):
+        reset()
+        backend.synchronize()
+        run(ev[s])
+        torch.cuda.synchronize()
     backend.synchronize()
     ms = total_ms / steps
     flops = 7 * dk * dv * hv * nseq * total
@@ -761,11 +796,20 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
     torch.cuda.synchronize()
     t0.record(stream)
     for s_ in range(steps):
-        run(ev[s_])
+        run()
     t1.record(stream)
     torch.cuda.synchronize()
     backend.synchronize()
     ms = t0.elapsed_time(t1) / steps
+    # per-call durations in a second pass (event markers between calls stall
+    # the queue, so they stay out of the timed region), after two unrecorded
+    # calls that bring the GPU back from idle
+    run()
+    run()
+    for s_ in range(steps):
+        run(ev[s_])
+    torch.cuda.synchronize()
+    backend.synchronize()
     call_us = np.array([x.elapsed_time(y) * 1e3 for x, y in ev])
     keys = sum(ctx_len + j + 1 for j in range(rows))  # per sequence, summed over rows
     nbytes = nseq * (ctx_len + rows) * kvh * dim * 2 * 2

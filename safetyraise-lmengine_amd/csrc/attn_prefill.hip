@@ -38,6 +38,7 @@
 // non-finite; the row is then flagged (kErrPrefillRange) for the host, which
 // recomputes the call on the f32 split-K path.
 #include <algorithm>
+#include <type_traits>
 
 #include "sr_device.hpp"
 
@@ -145,17 +146,78 @@ __device__ __forceinline__ float sum_f16x8(const f16x8 &x, float acc) {
 }
 
 // ---------------------------------------------------------------------------
-// K/V append of every new row: one workgroup per row.
+// K/V append of every new row.  16 lanes per (row, KV head), D/16 contiguous
+// elements per lane (one 16-byte load per tensor at D = 128), four heads per
+// wave; the KV heads of a row are consecutive waves.  Work items are
+// independent and short, so the whole call's loads are in flight together.
 // ---------------------------------------------------------------------------
+constexpr int kAppendHeadsPerWave = 4;
+
+// EPL consecutive activations (bf16 or f32) from element i on, widened to f32.
+template <int EPL>
+__device__ __forceinline__ void load_span(const void *base, size_t i, bool bf16, float (&x)[EPL]) {
+    if (bf16) {
+        const uint32_t *w = (const uint32_t *)((const uint16_t *)base + i);
+        if constexpr (EPL % 8 == 0) {
+#pragma unroll
+            for (int c = 0; c < EPL / 8; ++c) {
+                const u32x4 v = ((const u32x4 *)w)[c];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    x[8 * c + 2 * j] = bf16lo(v[j]);
+                    x[8 * c + 2 * j + 1] = bf16hi(v[j]);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < EPL / 2; ++j) {
+                const uint32_t v = w[j];
+                x[2 * j] = bf16lo(v);
+                x[2 * j + 1] = bf16hi(v);
+            }
+        }
+    } else {
+        const float4 *f = (const float4 *)((const float *)base + i);
+#pragma unroll
+        for (int c = 0; c < EPL / 4; ++c) {
+            const float4 v = f[c];
+            x[4 * c] = v.x;
+            x[4 * c + 1] = v.y;
+            x[4 * c + 2] = v.z;
+            x[4 * c + 3] = v.w;
+        }
+    }
+}
+
+// EPL f32 values rounded to bf16 and stored from element i on.
+template <int EPL>
+__device__ __forceinline__ void store_span_bf16(uint16_t *base, size_t i, const float (&x)[EPL]) {
+    uint32_t w[EPL / 2];
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) w[j] = pack_bf16x2(x[2 * j], x[2 * j + 1]);
+    if constexpr (EPL % 8 == 0) {
+#pragma unroll
+        for (int c = 0; c < EPL / 8; ++c) {
+            ((u32x4 *)(base + i))[c] = u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]};
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < EPL / 2; ++j) ((uint32_t *)(base + i))[j] = w[j];
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams p) {
-    constexpr int EPL = D / 64;
-    constexpr int kHeadBatch = 8;  // KV heads whose loads are in flight together
-    __shared__ float cs_s[4][128];
-    __shared__ float sn_s[4][128];
+    constexpr int EPL = D / 16;
+    constexpr int HW = kAppendHeadsPerWave;
+    __shared__ float cs_s[4][D / 2];
+    __shared__ float sn_s[4][D / 2];
+    __shared__ __align__(16) float xs[4][HW][D];  // normalised K, for the rotate-half partners
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = wave_index();
     const int lane = tid & 63;
+    const int slot = lane >> 4;  // head of the wave this lane works on
+    const int l16 = lane & 15;
     const PrefillMeta m = p.meta[blockIdx.y];
     // entries of this call's page-table update: block (0,0) writes them for
     // the kernels that follow; every row takes its own page from the list
@@ -165,14 +227,27 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
             ((int32_t *)p.page_table)[p.tbl_idx[i]] = p.tbl_val[i];
         }
     }
-    // one wave per row; no barrier below, so a wave past the rows just ends
-    const uint32_t r = blockIdx.x * 4 + wave;
+    // no barrier below, so a wave past the rows just ends
+    const uint32_t quads = (p.kv_heads + HW - 1) / HW;
+    const uint32_t w = blockIdx.x * 4 + wave;
+    const uint32_t r = w / quads;
+    const uint32_t quad = w - r * quads;
     if (r >= m.rows) return;
     const uint32_t row = m.row0 + r;
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const bool interleaved = (p.flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
+
+    const uint32_t kvh_raw = quad * HW + slot;
+    const bool head_ok = kvh_raw < p.kv_heads;
+    const uint32_t kvh = min(kvh_raw, p.kv_heads - 1);  // lanes past the heads repeat the last
+    const uint32_t e0 = l16 * EPL;                     // first element of this lane
+    const size_t src = ((size_t)row * p.kv_heads + kvh) * D + e0;
+    float x[EPL], vv[EPL], wk[EPL];
+    load_span<EPL>(p.k, src, bf16_in, x);
+    load_span<EPL>(p.v, src, bf16_in, vv);
+    load_span<EPL>(p.k_norm, e0, false, wk);  // readable without QK-norm too
 
     const uint32_t tok = m.ctx + r;
     const uint32_t tidx = m.slot * p.pages_per_seq + (tok >> p.log2_page_tokens);
@@ -185,86 +260,74 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     const uint32_t pt_mask = (1u << p.log2_page_tokens) - 1;
     const uint32_t half = p.rotary_dim / 2;
 
-    bool finite = true;
-    for (uint32_t kb = 0; kb < p.kv_heads; kb += kHeadBatch) {
-        // every load of the batch first (heads past kv_heads repeat the last)
-        float x[kHeadBatch][EPL], vv[kHeadBatch][EPL], wk[EPL];
+    // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with an IEEE
+    // f32 division (math.rs:90-91); each wave of the row computes the row's
+    // table, the first also saves it for the q side
+    const int32_t *pos3 = p.positions + (size_t)row * 3;
+    for (uint32_t i = lane; i < half; i += 64) {
+        const int axis = rope_axis(i, p.mrope, interleaved);
+        const float angle = (float)pos3[axis] / p.rope.denom[i];
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        cs_s[wave][i] = cs;
+        sn_s[wave][i] = sn;
+        if (quad == 0) p.rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
+    }
+    if (qk_norm) {
+        // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
+        float ss = 0.0f;
 #pragma unroll
-        for (int hh = 0; hh < kHeadBatch; ++hh) {
-            const uint32_t kvh = min(kb + hh, p.kv_heads - 1);
-            const size_t src = ((size_t)row * p.kv_heads + kvh) * D;
+        for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
+        ss = sum16(ss);
+        const float variance = ss / (float)D;
+        if (!isfinite(variance) && l16 == 0 && head_ok) atomicOr(p.err_word, kErrNonFiniteVariance);
+        const float inv = 1.0f / sqrtf(variance + p.eps);
 #pragma unroll
-            for (int i = 0; i < EPL; ++i) {
-                x[hh][i] = load_act_nb(p.k, src + lane + 64 * i, bf16_in);
-                vv[hh][i] = load_act_nb(p.v, src + lane + 64 * i, bf16_in);
-            }
-        }
+        for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (wk[i] + norm_add);
+    }
+    // rotate-half over the first rotary_dim dims (math.rs:52-99): element e
+    // pairs with e +- half, held by another lane of the same head; the
+    // partners go through this wave's LDS (LDS operations of one wave are
+    // performed in order, so no barrier is needed)
 #pragma unroll
-        for (int i = 0; i < EPL; ++i) wk[i] = p.k_norm[lane + 64 * i];  // readable without QK-norm too
-        if (kb == 0) {
-            // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with
-            // an IEEE f32 division (math.rs:90-91); once per row, shared with
-            // the q side (computed while the loads above are in flight)
-            const int32_t *pos3 = p.positions + (size_t)row * 3;
-            for (uint32_t i = lane; i < half; i += 64) {
-                const int axis = rope_axis(i, p.mrope, interleaved);
-                const float angle = (float)pos3[axis] / p.rope.denom[i];
-                float sn, cs;
-                sincosf(angle, &sn, &cs);
-                cs_s[wave][i] = cs;
-                sn_s[wave][i] = sn;
-                p.rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
-            }
-        }
+    for (int c = 0; c < EPL / 4; ++c) {
+        *(float4 *)&xs[wave][slot][e0 + 4 * c] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float y[EPL];
 #pragma unroll
-        for (int hh = 0; hh < kHeadBatch; ++hh) {
-            const uint32_t kvh = kb + hh;
-            if (kvh >= p.kv_heads) break;  // wave-uniform
-            if (qk_norm) {
-                // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
-                float ss = 0.0f;
-#pragma unroll
-                for (int i = 0; i < EPL; ++i) ss += x[hh][i] * x[hh][i];
-                ss = sum64(ss);
-                const float variance = ss / (float)D;
-                if (!isfinite(variance) && lane == 0) {
-                    atomicOr(p.err_word, kErrNonFiniteVariance);
-                }
-                const float inv = 1.0f / sqrtf(variance + p.eps);
-#pragma unroll
-                for (int i = 0; i < EPL; ++i) x[hh][i] = x[hh][i] * inv * (wk[i] + norm_add);
-            }
-            // rotate-half over the first rotary_dim dims (math.rs:52-99): dim
-            // e pairs with e +- half, which lives in lane (e +- half) % 64
-            float y[EPL];
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) {
-                const uint32_t e = lane + 64 * i;
-                y[i] = x[hh][i];
-                const uint32_t pe = e < half ? e + half : e - half;
-                float partner = 0.0f;
-#pragma unroll
-                for (int j = 0; j < EPL; ++j) {
-                    const float t = __shfl(x[hh][j], (int)(pe & 63));
-                    if ((int)(pe >> 6) == j) partner = t;
-                }
-                if (e < p.rotary_dim) {
-                    const uint32_t pi = e < half ? e : e - half;
-                    y[i] = e < half ? x[hh][i] * cs_s[wave][pi] - partner * sn_s[wave][pi]
-                                    : x[hh][i] * cs_s[wave][pi] + partner * sn_s[wave][pi];
-                }
-            }
-            const size_t dst =
-                ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D;
-#pragma unroll
-            for (int i = 0; i < EPL; ++i) {
-                finite = finite && isfinite(y[i]) && isfinite(vv[hh][i]);
-                p.k_pages[dst + lane + 64 * i] = f32_to_bf16(y[i]);
-                p.v_pages[dst + lane + 64 * i] = f32_to_bf16(vv[hh][i]);
-            }
+    for (int i = 0; i < EPL; ++i) {
+        const uint32_t e = e0 + i;
+        y[i] = x[i];
+        if (e < p.rotary_dim) {
+            const bool lo = e < half;
+            const uint32_t pi = lo ? e : e - half;
+            const float partner = xs[wave][slot][lo ? e + half : e - half];
+            const float cs = cs_s[wave][pi], sn = sn_s[wave][pi];
+            y[i] = lo ? x[i] * cs - partner * sn : x[i] * cs + partner * sn;
         }
     }
-    if (!finite) atomicOr(p.err_word, kErrNonFiniteKv);
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) finite = finite && isfinite(y[i]) && isfinite(vv[i]);
+    if (head_ok) {
+        const size_t dst = ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D + e0;
+        store_span_bf16<EPL>(p.k_pages, dst, y);
+        store_span_bf16<EPL>(p.v_pages, dst, vv);
+    }
+    if (__builtin_amdgcn_ballot_w64(head_ok && !finite) != 0 && lane == 0) {
+        atomicOr(p.err_word, kErrNonFiniteKv);
+    }
+}
+
+// One call's append: (rows x head quads) waves, four per workgroup.
+template <int D>
+void launch_append(hipStream_t stream, const PrefillParams &p, uint32_t max_rows) {
+    const uint32_t quads = (p.kv_heads + kAppendHeadsPerWave - 1) / kAppendHeadsPerWave;
+    const uint32_t waves = max_rows * quads;
+    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3((waves + 3) / 4, p.nseq), dim3(256), 0, stream, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -290,6 +353,11 @@ __device__ __forceinline__ uint32_t k_swz(uint32_t key) {
 __device__ __forceinline__ uint32_t vt_swz(uint32_t d) {
     return ((d >> 1) & 7) ^ ((d & 1) << 2) ^ ((d >> 4) & 7);
 }
+// Row-major V tiles ([64 keys][D] fp16, like K) read by transposing loads:
+// unit c of key row r sits at unit c ^ ((r & 3) << 2), so that one
+// transposing read (8 rows x 4 units, 16 lanes per 4 rows x 2 units) meets
+// every bank once per half wave.
+__device__ __forceinline__ uint32_t v_swz(uint32_t key) { return (key & 3u) << 2; }
 
 // Where one workgroup's rows are: (sequence, KV head, row block) from the
 // block index, with the KV head fastest (the 8 XCDs take consecutive blocks,
@@ -515,6 +583,35 @@ struct LeanIo {
             const uint32_t g = u / KCH;
 #pragma unroll
             for (int j = 0; j < 4; ++j) r[4 * i + j] = *(const u32x4 *)(v_pages + row(t, base, 4 * g + j) + ch * 8);
+        }
+    }
+    // K (is_v false) or V (is_v true) rows of tile t in the K layout of
+    // load_k, as one instruction stream: only the source differs, so there is
+    // no branch whose two sides would load into the same registers (the
+    // compiler then waits for every load in flight where the sides meet)
+    template <int N>
+    __device__ __forceinline__ void load_kv(u32x4 (&r)[N], uint32_t t, size_t base, uint32_t gt,
+                                            bool is_v) const {
+        static_assert(N >= KL, "staging registers");
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+        const uint16_t *src = is_v ? v_pages : k_pages;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) r[i] = *(const u32x4 *)(src + row(t, base, k0 + i * KSTEP) + ch * 8);
+    }
+    // V rows loaded by load_kv as the row-major fp16 image (v_swz); rows from
+    // valid_keys on become 0
+    template <int N>
+    __device__ __forceinline__ void store_v_rows(const u32x4 (&r)[N], unsigned char *vt,
+                                                 uint32_t valid_keys, uint32_t gt) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const uint32_t key = k0 + i * KSTEP;
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(r[i][j]), bf16hi(r[i][j]));
+            if (key >= valid_keys) f = u32x4{0, 0, 0, 0};
+            *(u32x4 *)(vt + key * (D * 2) + ((ch ^ v_swz(key)) * 16)) = f;
         }
     }
     template <int N>
@@ -764,6 +861,55 @@ __device__ __forceinline__ void pv_tile(const unsigned char *vt, const f16x8 (&p
     }
 }
 
+// The same product from a row-major V tile (v_swz): the A operand of lane
+// (d = col, half h) for k-step st is V[keys 16 st + 4 h + {0..3, 8..11}][d],
+// two transposing reads.  In each 16-lane group (g = lane / 16) lane s points
+// at row 4 (s / 4) + ... and columns 4 (s % 4) .. + 3 of the group's 16
+// columns; the read hands lane i of the group column i of those 4 rows.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// Byte offset of lane's transposing reads in a V tile, per 32-column tile
+// (k-step 0, first read; the other reads add 16 st and 8 rows).
+template <int D>
+__device__ __forceinline__ void pv_rows_offsets(int lane, uint32_t (&off)[D / 32]) {
+    static_assert(D == 128, "unit index: 16 units per row, 4 column tiles");
+    const uint32_t s = lane & 15, g = lane >> 4;
+    const uint32_t row = 4 * (g >> 1) + (s >> 2);
+#pragma unroll
+    for (int tt = 0; tt < D / 32; ++tt) {
+        const uint32_t unit = (((uint32_t)tt ^ (s >> 2)) << 2) | ((g & 1) << 1) | ((s >> 1) & 1);
+        off[tt] = row * (D * 2) + unit * 16 + (s & 1) * 8;
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void pv_tile_rows(const unsigned char *vt, const uint32_t (&off)[D / 32],
+                                             const f16x8 (&pop)[4], f32x16 (&oacc)[D / 32]) {
+    constexpr int NT = D / 32;
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    auto v_frag = [&](int tt, int st) __attribute__((always_inline)) -> f16x8 {
+        const unsigned char *b = vt + off[tt] + st * 16 * (D * 2);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(b));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(b + 8 * (D * 2)));
+        return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    f16x8 va[2][NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) va[0][tt] = v_frag(tt, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            if (st + 1 < 4) va[(st + 1) & 1][tt] = v_frag(tt, st + 1);
+            oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va[st & 1][tt], pop[st], oacc[tt], 0,
+                                                              0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // Online softmax of one tile (math.rs:133-148 in the log2 domain): causal
 // mask, row max across the two lane halves, P = 2^(s - m) in fp16, row sum of
 // those fp16 values, lazy rescale of O (only when some row's max moved).
@@ -940,16 +1086,19 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
 //   group 0  M(t)      V(t)        M(t+1)
 //   group 1  V(t-1)    M(t)        V(t)
 //
-// Group 0 converts and stores K tiles, group 1 V tiles, each loading its next
-// tile into registers two phases ahead.  K(t) is read in phases 2t and 2t+1
-// and K(t+2) written in phase 2t+3: two K buffers.  V(t) is read in phases
-// 2t+2 and 2t+3 while V(t+2) is written in phase 2t+2: three V buffers.
+// Group 0 converts and stores K tiles, group 1 V tiles, both as row-major
+// fp16 images (the PV product reads V with transposing loads); each group
+// loads its next tile into registers one step ahead.  Step t stores tile t+1:
+// K(t+1) in phase 2t+1, V(t+1) in phase 2t+2.  K(t) is read in phases 2t and
+// 2t+1, V(t) in phases 2t+2 and 2t+3, so the tile a store replaces (two
+// tiles back) is no longer read: two buffers of each, tile j in buffer j & 1,
+// and the loop's two halves address them with constant offsets.
 // Every wave passes the same number of barriers (group 1 one extra at the
 // start, group 0 one extra at the end).
 // One workgroup = 2 x 4 waves = (G heads x 4/G blocks of 32 rows) per group.
 // ---------------------------------------------------------------------------
 template <int D>
-constexpr size_t kPingPongLds = 5 * kTileBytes<D>;  // K x 2, V x 3
+constexpr size_t kPingPongLds = 4 * kTileBytes<D>;  // K x 2, V x 2
 
 template <int D, int G, bool kTilePage>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void
@@ -958,13 +1107,13 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     constexpr int NS = D / 16;
     constexpr int NT = D / 32;
     using Io = LeanIo<D, 256, kTilePage>;
-    constexpr int SL = (Io::KL > 4 * Io::VL) ? Io::KL : 4 * Io::VL;
+    constexpr int SL = Io::KL;
     extern __shared__ __align__(16) unsigned char lds[];
     unsigned char *kbuf = lds;                         // 2 K tiles
-    unsigned char *vbuf = lds + 2 * kTileBytes<D>;     // 3 V^T tiles
+    unsigned char *vbuf = lds + 2 * kTileBytes<D>;     // 2 V tiles
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = wave_index();
     const int lane = tid & 63;
     const int h = lane >> 5;
     const int col = lane & 31;
@@ -988,25 +1137,24 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     // staging registers, two sets: tile j's data lives in stage[j & 1], so a
     // load never waits for the LDS stores that read the other set
     u32x4 stage0[SL] = {}, stage1[SL] = {};
-    // tile 0: K by group 0, V by group 1; then each group's tile 1 in flight
     // tiles 0 and 1 (K by group 0, V by group 1) and tile 2's page id are
-    // requested before the q prologue, so their latency overlaps it
+    // requested before the q prologue, so their latency overlaps it.  The
+    // page id goes first: in the loop it is consumed with one tile's loads
+    // issued after it, and a wait that must also cover this path can then
+    // still leave those loads in flight.
+    uint32_t pg_next = io.page_of(2);
     {
         const uint32_t pg0 = io.page_of(0), pg1 = io.page_of(1);
         const size_t tb0 = io.tile_base(0, pg0), tb1 = io.tile_base(min(1u, n - 1), pg1);
-        if (grp == 0) {
-            io.load_k(stage0, 0, tb0, gt0);
-            io.load_k(stage1, min(1u, n - 1), tb1, gt0);
-        } else {
-            io.load_v(stage0, 0, tb0, gt0);
-            io.load_v(stage1, min(1u, n - 1), tb1, gt0);
-        }
+        io.load_kv(stage0, 0, tb0, gt0, grp != 0);
+        io.load_kv(stage1, min(1u, n - 1), tb1, gt0, grp != 0);
     }
-    uint32_t pg_next = io.page_of(2);
     f16x8 qop[NS];
     q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
     if (grp == 0) io.store_k(stage0, kbuf, gt0);
-    else io.store_v(stage0, vbuf, b.n_keys, gt0);
+    else io.store_v_rows(stage0, vbuf, b.n_keys, gt0);
+    uint32_t voff[NT];
+    pv_rows_offsets<D>(lane, voff);
     f32x16 oacc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
@@ -1016,19 +1164,22 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     __syncthreads();
     if (grp == 1) __syncthreads();  // group 1 starts one phase later
 
-    // one iteration for tile t: `cur` holds tile t+1 (stored now), `nxt`
-    // receives tile t+2
-    auto step = [&](uint32_t t, u32x4 (&cur)[SL], u32x4 (&nxt)[SL]) __attribute__((always_inline)) {
+    // one iteration for tile t (t & 1 == PAR): `cur` holds tile t+1 (stored
+    // now), `nxt` receives tile t+2
+    auto step = [&](uint32_t t, auto par, u32x4 (&cur)[SL], u32x4 (&nxt)[SL])
+                    __attribute__((always_inline)) {
+        constexpr uint32_t PAR = decltype(par)::value;
         // ---- M phase: PV(t-1), S(t) ----
-        if (t > 0) pv_tile<D>(vbuf + ((t - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
+        if (t > 0) pv_tile_rows<D>(vbuf + (PAR ^ 1) * kTileBytes<D>, voff, pop, oacc);
         f32x16 sacc[2];
-        s_tile<D>(kbuf + (t & 1) * kTileBytes<D>, qop, h, col, sacc);
+        s_tile<D>(kbuf + PAR * kTileBytes<D>, qop, h, col, sacc);
         __syncthreads();
         // ---- V phase: softmax(t), stage the group's tile t+1, load t+2 ----
         // The page id of tile t+2 (requested one phase earlier) is consumed
         // here, before this phase's LDS stores are issued, so that its wait
         // does not also wait for them.  Then tile t+3's is requested.
-        size_t tb_next = io.tile_base(t + 2, pg_next);
+        const uint32_t t_next = min(t + 2, n - 1);
+        size_t tb_next = io.tile_base(t_next, pg_next);
         pin(tb_next);
         pg_next = io.page_of(t + 3);
         const uint32_t key0 = t * kKeyTile;
@@ -1037,13 +1188,13 @@ attn_prefill_pp_kernel(const PrefillParams p) {
         uint32_t gt = gt0;
         pin(gt);
         if (t + 1 < n) {
-            if (grp == 0) io.store_k(cur, kbuf + ((t + 1) & 1) * kTileBytes<D>, gt);
-            else io.store_v(cur, vbuf + ((t + 1) % 3) * kTileBytes<D>, b.n_keys - key0 - kKeyTile, gt);
-            if (t + 2 < n) {
-                if (grp == 0) io.load_k(nxt, t + 2, tb_next, gt);
-                else io.load_v(nxt, t + 2, tb_next, gt);
-            }
+            if (grp == 0) io.store_k(cur, kbuf + (PAR ^ 1) * kTileBytes<D>, gt);
+            else io.store_v_rows(cur, vbuf + (PAR ^ 1) * kTileBytes<D>, b.n_keys - key0 - kKeyTile, gt);
         }
+        // issued on every path (past the end, the last tile again): a load
+        // skipped on some path would make the next wait for an older load
+        // (the page id) wait for every load in flight
+        io.load_kv(nxt, t_next, tb_next, gt, grp != 0);
         // the softmax results stay in this phase
 #pragma unroll
         for (int st = 0; st < 4; ++st) pin(pop[st]);
@@ -1051,11 +1202,18 @@ attn_prefill_pp_kernel(const PrefillParams p) {
         for (int tt = 0; tt < NT; ++tt) pin(oacc[tt]);
         __syncthreads();
     };
-    for (uint32_t t = 0; t < n; t += 2) {
-        step(t, stage1, stage0);
-        if (t + 1 < n) step(t + 1, stage0, stage1);
+    // both halves on every trip round the loop, the odd tile after it: a
+    // path that skipped the second half and went round again would reach
+    // the first half with that half's own loads still in flight
+    uint32_t t = 0;
+    using Even = std::integral_constant<uint32_t, 0>;
+    using Odd = std::integral_constant<uint32_t, 1>;
+    for (; t + 1 < n; t += 2) {
+        step(t, Even{}, stage1, stage0);
+        step(t + 1, Odd{}, stage0, stage1);
     }
-    pv_tile<D>(vbuf + ((n - 1) % 3) * kTileBytes<D>, pop, h, col, oacc);
+    if (t < n) step(t, Even{}, stage1, stage0);
+    pv_tile_rows<D>(vbuf + ((n - 1) & 1) * kTileBytes<D>, voff, pop, oacc);
     if (grp == 0) __syncthreads();  // matches group 1's extra barrier
 
     const uint32_t row = wrow0 + col;
@@ -1115,7 +1273,7 @@ hipError_t launch_dg(hipStream_t stream, PrefillParams &p, const SeqMeta *seqs, 
         max_rows = std::max(max_rows, m.rows);
     }
     p.max_blk = max_blk;
-    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3((max_rows + 3) / 4, p.nseq), dim3(256), 0, stream, p);
+    launch_append<D>(stream, p, max_rows);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t blocks = p.max_blk * p.nseq * p.kv_heads;
@@ -1259,7 +1417,7 @@ attn_verify_kernel(const VerifyParams vp) {
     const PrefillParams &p = vp.p;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int wave = wave_index();
     const int lane = tid & 63;
     const uint32_t kvh = blockIdx.x % p.kv_heads;
     const uint32_t j = blockIdx.x / p.kv_heads;
@@ -1606,8 +1764,8 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
     vp.partials = in.reserve_partials((size_t)records * stride * sizeof(float));
     if (vp.partials == nullptr) return hipErrorOutOfMemory;
     // K/V of the new rows and their RoPE cos/sin first (append kernel)
-    hipLaunchKernelGGL(a.head_dim == 64 ? kv_append_rows_kernel<64> : kv_append_rows_kernel<128>,
-                       dim3((max_rows + 3) / 4, p.nseq), dim3(256), 0, stream, p);
+    if (a.head_dim == 64) launch_append<64>(stream, p, max_rows);
+    else launch_append<128>(stream, p, max_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t grid = blocks * a.kv_heads;

@@ -53,6 +53,14 @@ __device__ __forceinline__ float load_act_nb(const void *p, size_t i, bool bf16)
     return __uint_as_float(bits);
 }
 
+// Index of the calling wave in its workgroup, in a scalar register: branches
+// on it are scalar branches, so a wave runs only its own side of an
+// if/else instead of both under an exec mask (where registers one side loads
+// into and the other reuses would cost a wait for every load in flight).
+__device__ __forceinline__ int wave_index() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 // DPP controls (gfx9 encoding): quad permutes, half-row and row mirrors.
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
