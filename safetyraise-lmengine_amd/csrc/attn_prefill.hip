@@ -598,20 +598,23 @@ struct LeanIo {
 #pragma unroll
         for (int i = 0; i < KL; ++i) r[i] = *(const u32x4 *)(src + row(t, base, k0 + i * KSTEP) + ch * 8);
     }
-    // V rows loaded by load_kv as the row-major fp16 image (v_swz); rows from
-    // valid_keys on become 0
+    // V rows loaded by load_kv as the row-major fp16 image (v_swz).  Rows
+    // from valid_keys on (past the last key: their probabilities are 0, but
+    // the page may hold non-finite leftovers) become 0; only a partial tile
+    // pays for that.
     template <int N>
     __device__ __forceinline__ void store_v_rows(const u32x4 (&r)[N], unsigned char *vt,
                                                  uint32_t valid_keys, uint32_t gt) const {
         const uint32_t ch = gt % KCH, k0 = gt / KCH;
+        const bool partial = valid_keys < (uint32_t)kKeyTile;  // uniform
 #pragma unroll
         for (int i = 0; i < KL; ++i) {
-            const uint32_t key = k0 + i * KSTEP;
+            const uint32_t key = k0 + i * KSTEP;  // key & 3 == k0 & 3
             u32x4 f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(r[i][j]), bf16hi(r[i][j]));
-            if (key >= valid_keys) f = u32x4{0, 0, 0, 0};
-            *(u32x4 *)(vt + key * (D * 2) + ((ch ^ v_swz(key)) * 16)) = f;
+            if (partial && key >= valid_keys) f = u32x4{0, 0, 0, 0};
+            *(u32x4 *)(vt + key * (D * 2) + ((ch ^ v_swz(k0)) * 16)) = f;
         }
     }
     template <int N>
