@@ -81,17 +81,24 @@ struct Frag {
     uint32_t w[DPL / 2];
 };
 
+// Cache pages are streamed once per call: the loads are nontemporal (the
+// lines are not kept for reuse), which measured ~8 % more read bandwidth on
+// MI355X than ordinary loads in a plain streaming kernel (5.9-6.0 vs
+// 5.4-5.7 TB/s).
+typedef uint32_t nt_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t nt_u32x4 __attribute__((ext_vector_type(4)));
+
 template <int DPL>
 __device__ __forceinline__ Frag<DPL> load_frag(const uint16_t *p) {
     Frag<DPL> f;
     if constexpr (DPL == 4) {
-        const uint2 x = *(const uint2 *)p;
+        const nt_u32x2 x = __builtin_nontemporal_load((const nt_u32x2 *)p);
         f.w[0] = x.x;
         f.w[1] = x.y;
     } else {
 #pragma unroll
         for (int i = 0; i < DPL / 8; ++i) {
-            const uint4 x = *((const uint4 *)p + i);
+            const nt_u32x4 x = __builtin_nontemporal_load((const nt_u32x4 *)p + i);
             f.w[4 * i + 0] = x.x;
             f.w[4 * i + 1] = x.y;
             f.w[4 * i + 2] = x.z;
