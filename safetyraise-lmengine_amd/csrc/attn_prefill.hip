@@ -730,11 +730,16 @@ __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_
         }
     }
     if (qk_norm) {
-        float ss = 0.0f;
+        // eight partial sums: a chain of 64 dependent FMAs would sit on the
+        // prologue's critical path
+        float part[8];
 #pragma unroll
-        for (int st = 0; st < NS; ++st)
+        for (int j = 0; j < 8; ++j) part[j] = x[0][j] * x[0][j];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ss += x[st][j] * x[st][j];
+        for (int st = 1; st < NS; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part[j] += x[st][j] * x[st][j];
+        float ss = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
         ss = xhalf_sum(ss);
         const float variance = ss / (float)D;
         if (!isfinite(variance) && lane == 0) {
@@ -913,6 +918,15 @@ __device__ __forceinline__ void pv_tile_rows(const unsigned char *vt, const uint
     }
 }
 
+// max(a, b, c) as one v_max3_f32, without the quieting of signalling NaNs
+// that fmaxf adds per operand (the scores come from MFMAs; a NaN score makes
+// the row non-finite either way)
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Online softmax of one tile (math.rs:133-148 in the log2 domain): causal
 // mask, row max across the two lane halves, P = 2^(s - m) in fp16, row sum of
 // those fp16 values, lazy rescale of O (only when some row's max moved).
@@ -930,11 +944,20 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&sacc)[2], uint32_t key0, b
                 if (key > key_limit) sacc[u][i] = -INFINITY;
             }
     }
-    float mx = sacc[0][0];
+    // row max as a tree: 16 v_max3 at depth 4 instead of a chain of 16
+    float m11[11];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[u][i]);
+    for (int j = 0; j < 10; ++j) {
+        const int e = 3 * j;
+        m11[j] = max3_raw(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15],
+                          sacc[(e + 2) >> 4][(e + 2) & 15]);
+    }
+    m11[10] = max3_raw(sacc[1][14], sacc[1][15], sacc[1][15]);
+    const float m4a = max3_raw(m11[0], m11[1], m11[2]);
+    const float m4b = max3_raw(m11[3], m11[4], m11[5]);
+    const float m4c = max3_raw(m11[6], m11[7], m11[8]);
+    const float m4d = max3_raw(m11[9], m11[10], m11[10]);
+    float mx = max3_raw(max3_raw(m4a, m4b, m4c), m4d, m4d);
     mx = xhalf_max(mx);
     // the reference max is only raised when it grows by more than
     // kLazyRescale (log2 units): P stays <= 2^kLazyRescale (exact range for
