@@ -1435,7 +1435,7 @@ struct VerifyIo {
 // pair 32 of the query vectors.  One barrier per step: after barrier k, the
 // tiles of step k are in LDS and the buffers of step k-1 are free.  Each
 // pair leaves its own record, so a partition has two.
-constexpr int kVerifyDepth = 2;
+constexpr int kVerifyDepth = 3;
 constexpr int kVerifyThreads = 512;
 
 template <int D>
