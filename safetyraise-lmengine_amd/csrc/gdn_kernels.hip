@@ -308,10 +308,12 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         bv = load_act_nb(p.b, row * p.value_heads + h, bf16_in);
     };
     load_row(m.row0);
-    // state rows v = (NTH/16) i + group, dims [8 l16, 8 l16 + 8); requested after
+    // state rows v = (NTH/16) i + group, dims [4 l16, 4 l16 + 4) and
+    // [64 + 4 l16, 64 + 4 l16 + 4): each 16-byte load or store instruction
+    // then covers 256 contiguous bytes of a row; requested after
     // the (branchy) conv loads so that nothing waits for them before the
     // delta step itself
-    float *sbase = p.state + ((size_t)m.slot * p.value_heads + h) * kHeadDv * kDk + l16 * 8;
+    float *sbase = p.state + ((size_t)m.slot * p.value_heads + h) * kHeadDv * kDk + l16 * 4;
     // the state is read once and written once per call: nontemporal
     // accesses (streaming reads measured ~8 % faster than ordinary loads)
     typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
@@ -320,7 +322,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     for (int i = 0; i < RPG; ++i) {
         const float *src = sbase + (size_t)((NTH / 16) * i + group) * kDk;
         const nt_f32x4 x0 = __builtin_nontemporal_load((const nt_f32x4 *)src);
-        const nt_f32x4 x1 = __builtin_nontemporal_load((const nt_f32x4 *)(src + 4));
+        const nt_f32x4 x1 = __builtin_nontemporal_load((const nt_f32x4 *)(src + kDk / 2));
         S[i][0] = x0.x; S[i][1] = x0.y; S[i][2] = x0.z; S[i][3] = x0.w;
         S[i][4] = x1.x; S[i][5] = x1.y; S[i][6] = x1.z; S[i][7] = x1.w;
     }
@@ -359,8 +361,9 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         float kh8[8], qh8[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            kh8[j] = conv_s[kDk + l16 * 8 + j] * ki;
-            qh8[j] = conv_s[l16 * 8 + j] * qi;
+            const int dim = (j < 4) ? 4 * l16 + j : kDk / 2 + 4 * l16 + (j - 4);
+            kh8[j] = conv_s[kDk + dim] * ki;
+            qh8[j] = conv_s[dim] * qi;
         }
 #pragma unroll
         for (int i = 0; i < RPG; ++i) {
@@ -388,7 +391,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
                 __builtin_nontemporal_store(nt_f32x4{S[i][0], S[i][1], S[i][2], S[i][3]},
                                             (nt_f32x4 *)dst);
                 __builtin_nontemporal_store(nt_f32x4{S[i][4], S[i][5], S[i][6], S[i][7]},
-                                            (nt_f32x4 *)(dst + 4));
+                                            (nt_f32x4 *)(dst + kDk / 2));
             }
         }
         __syncthreads();
