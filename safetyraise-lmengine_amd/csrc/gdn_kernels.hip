@@ -603,13 +603,15 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParam
 #pragma unroll
     for (int j = 0; j < KW - 1; ++j) hv[j] = p.history[(hist_slot + ch1) * K1 + min(j, max(Kr - 2, 0))];
 
-    // state slice -> LDS (16 floats per thread)
+    // state slice -> LDS (16 floats per thread, as 4 spans of 4 that are 32
+    // floats apart: each 16-byte access instruction covers 128 contiguous
+    // bytes of a row)
     float *state = p.state + (((size_t)m.slot * p.value_heads + h) * p.value_dim + vq * kVs) * kDk;
     {
-        const int v = tid >> 3, d0 = (tid & 7) * 16;
+        const int v = tid >> 3, d0 = (tid & 7) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            *(float4 *)&L.s0[v][d0 + 4 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 4 * i);
+            *(float4 *)&L.s0[v][d0 + 32 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 32 * i);
         }
     }
     const float a_log_e = expf(p.a_log[h]);
@@ -990,12 +992,12 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParam
             __syncthreads();  // the next chunk reads S0 and rewrites q, k, pm, ...
         }
     }
-    // state slice and history back
+    // state slice and history back (the same spans as the load)
     {
-        const int v = tid >> 3, d0 = (tid & 7) * 16;
+        const int v = tid >> 3, d0 = (tid & 7) * 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            *(float4 *)(state + (size_t)v * kDk + d0 + 4 * i) = *(const float4 *)&L.s0[v][d0 + 4 * i];
+            *(float4 *)(state + (size_t)v * kDk + d0 + 32 * i) = *(const float4 *)&L.s0[v][d0 + 32 * i];
         }
     }
     const bool owns_qk = (h % groups == 0) && vq == 0;
