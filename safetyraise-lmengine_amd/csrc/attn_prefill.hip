@@ -1363,33 +1363,46 @@ struct VerifyIo {
     static constexpr int KSTEP = 128 / KCH;                 // keys per pass of the lanes
     static constexpr int KL = kKeyTile / KSTEP;             // K chunks per lane
     static constexpr int VL = kKeyTile / 4 / KSTEP;         // 4-key V units per lane
-    const uint16_t *k_pages;
-    const uint16_t *v_pages;
+    const unsigned char *k_head;  // page 0 of this KV head in the K pool
+    const unsigned char *v_head;
     const int32_t *pids;  // page ids from page `first` on (LDS)
-    size_t head_base;
+    uint32_t page_bytes;  // page_tokens * D * 2
     uint32_t lpt, pt_mask, first, last_tok;
 
-    __device__ __forceinline__ size_t row(uint32_t tok) const {
-        tok = min(tok, last_tok);  // keys past the sequence's last are masked
-        return (((head_base + (uint32_t)pids[(tok >> lpt) - first]) << lpt) + (tok & pt_mask)) * D;
+    // byte address of 16-byte chunk ch of token tok's row on page pg
+    __device__ __forceinline__ const u32x4 *row_ptr(const unsigned char *head, uint32_t pg,
+                                                   uint32_t tok, uint32_t ch) const {
+        return (const u32x4 *)(head + ((uint64_t)pg * page_bytes +
+                                       ((tok & pt_mask) * (uint32_t)(D * 2) + ch * 16)));
     }
     __device__ __forceinline__ void load(u32x4 (&kr)[KL], u32x4 (&vr)[4 * VL], uint32_t t,
                                          uint32_t gt) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+        const uint32_t key0 = t * kKeyTile;
+        // keys past the sequence's last are masked: they read its last row.
+        // A 4-key V group never straddles a page, and neither does its clamp.
+        uint32_t tk[KL], tv[VL], pk[KL], pv[VL];
+#pragma unroll
+        for (int i = 0; i < KL; ++i) tk[i] = min(key0 + k0 + i * KSTEP, last_tok);
+#pragma unroll
+        for (int i = 0; i < VL; ++i) tv[i] = min(key0 + 4 * (k0 + i * KSTEP), last_tok);
+        // every page id is requested before any is used: one LDS round trip
+        // per tile instead of one per load
+#pragma unroll
+        for (int i = 0; i < KL; ++i) pk[i] = (uint32_t)pids[(tk[i] >> lpt) - first];
+#pragma unroll
+        for (int i = 0; i < VL; ++i) pv[i] = (uint32_t)pids[(tv[i] >> lpt) - first];
+        __builtin_amdgcn_sched_barrier(0);
         // every tile is read by one workgroup once: nontemporal loads
         // (streaming reads measured ~8 % faster than ordinary loads)
-        const uint32_t ch = gt % KCH, k0 = gt / KCH;
 #pragma unroll
-        for (int i = 0; i < KL; ++i) {
-            kr[i] = __builtin_nontemporal_load(
-                (const u32x4 *)(k_pages + row(t * kKeyTile + k0 + i * KSTEP) + ch * 8));
-        }
+        for (int i = 0; i < KL; ++i) kr[i] = __builtin_nontemporal_load(row_ptr(k_head, pk[i], tk[i], ch));
 #pragma unroll
         for (int i = 0; i < VL; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t key = 4 * (k0 + i * KSTEP) + j;
-                vr[4 * i + j] = __builtin_nontemporal_load(
-                    (const u32x4 *)(v_pages + row(t * kKeyTile + key) + ch * 8));
+                const uint32_t tok = min(key0 + 4 * (k0 + i * KSTEP) + j, last_tok);
+                vr[4 * i + j] = __builtin_nontemporal_load(row_ptr(v_head, pv[i], tok, ch));
             }
     }
     // valid_keys: keys of the tile that exist; V rows past them become 0
@@ -1475,11 +1488,12 @@ attn_verify_kernel(const VerifyParams vp) {
         const uint32_t q = pt >> 7;     // which tile of the step
         const uint32_t gt0 = pt & 127;
         VerifyIo<D> io;
-        io.k_pages = p.k_pages;
-        io.v_pages = p.v_pages;
-        io.head_base = (size_t)kvh * p.num_pages;
         io.lpt = p.log2_page_tokens;
         io.pt_mask = (1u << io.lpt) - 1;
+        io.page_bytes = (D * 2) << io.lpt;
+        const size_t head_bytes = (size_t)kvh * p.num_pages * io.page_bytes;
+        io.k_head = (const unsigned char *)p.k_pages + head_bytes;
+        io.v_head = (const unsigned char *)p.v_pages + head_bytes;
         io.last_tok = total - 1;
         // the page ids of the partition's keys go to LDS once, so that no
         // tile load waits on a page-table read
