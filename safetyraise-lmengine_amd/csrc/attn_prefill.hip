@@ -1405,10 +1405,12 @@ struct VerifyIo {
                 vr[4 * i + j] = __builtin_nontemporal_load(row_ptr(v_head, pv[i], tok, ch));
             }
     }
-    // valid_keys: keys of the tile that exist; V rows past them become 0
+    // Keys past the sequence's last were loaded as copies of its last row
+    // (load clamps them), so their V rows are finite and need no zeroing: the
+    // consumers mask their scores, and P = 0 times a finite value adds 0.
     __device__ __forceinline__ void store(const u32x4 (&kr)[KL], const u32x4 (&vr)[4 * VL],
                                           unsigned char *kt, unsigned char *vt,
-                                          uint32_t valid_keys, uint32_t gt) const {
+                                          uint32_t gt) const {
         const uint32_t ch = gt % KCH, k0 = gt / KCH;
 #pragma unroll
         for (int i = 0; i < KL; ++i) {
@@ -1421,11 +1423,7 @@ struct VerifyIo {
 #pragma unroll
         for (int i = 0; i < VL; ++i) {
             const uint32_t g = k0 + i * KSTEP;
-            u32x4 w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                w[j] = (4 * g + j < valid_keys) ? vr[4 * i + j] : u32x4{0, 0, 0, 0};
-            }
+            const u32x4 *w = vr + 4 * i;
             const uint32_t unit = 2 * (g >> 2) + (g & 1);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1501,7 +1499,17 @@ attn_verify_kernel(const VerifyParams vp) {
         const int32_t *table = p.page_table + (size_t)m.slot * p.pages_per_seq;
         io.first = key_begin >> io.lpt;
         const uint32_t n = ((key_end - 1) >> io.lpt) - io.first + 1;
-        for (uint32_t i = pt; i < n; i += 256) pids[i] = table[io.first + i];
+        // all of a lane's table reads are in flight before the first LDS
+        // store (past n, the last entry again: in bounds, never stored)
+        int32_t pw[kVerifyPageSlots / 256];
+#pragma unroll
+        for (uint32_t u = 0; u < kVerifyPageSlots / 256; ++u) {
+            pw[u] = table[io.first + min(pt + 256 * u, n - 1)];
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kVerifyPageSlots / 256; ++u) {
+            if (pt + 256 * u < n) pids[pt + 256 * u] = pw[u];
+        }
         io.pids = pids;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_barrier();  // (A) the producers share pids
@@ -1523,8 +1531,7 @@ attn_verify_kernel(const VerifyParams vp) {
                 const uint32_t k = kb + u;
                 unsigned char *kt = tile_lds(k, q);
                 // tiles past t1 store a repeat of the last tile nobody reads
-                const uint32_t key0 = min(t0 + 2 * k + q, t1 - 1) * kKeyTile;
-                io.store(kreg[u], vreg[u], kt, kt + kTileBytes<D>, key_end - key0, gt);
+                io.store(kreg[u], vreg[u], kt, kt + kTileBytes<D>, gt);
                 __syncthreads();  // (B) the tiles of step k are in LDS
                 io.load(kreg[u], vreg[u], min(t0 + 2 * (k + kVerifyDepth) + q, t1 - 1), gt);
                 __builtin_amdgcn_sched_barrier(0);
