@@ -673,10 +673,10 @@ struct QArgs {
 
 __device__ __forceinline__ QArgs q_args(const PrefillParams &p) {
     QArgs a{p.q, p.q_norm, p.rope_cs, p.err_word, p.flags, p.rotary_dim, p.eps};
-    pin_s(a.q);
-    pin_s(a.q_norm);
-    pin_s(a.rope_cs);
-    pin_s(a.err_word);
+    a.q = pin_global(a.q);
+    a.q_norm = pin_global(a.q_norm);
+    a.rope_cs = pin_global(a.rope_cs);
+    a.err_word = pin_global(a.err_word);
     pin_s(a.flags);
     pin_s(a.rotary_dim);
     pin_s(a.eps);

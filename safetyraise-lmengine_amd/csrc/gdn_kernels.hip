@@ -251,6 +251,43 @@ __global__ void __launch_bounds__(kThreads) gdn_delta_kernel(const GdnParams p) 
 // the sequences x heads workgroups fill the GPU.
 // ---------------------------------------------------------------------------
 constexpr int kHeadDv = 128;
+
+// The kernel arguments gdn_head_kernel uses, held in scalar registers.
+struct HeadArgs {
+    float *state;
+    float *history;
+    const void *qkv;
+    const void *a;
+    const void *b;
+    const float *a_log;
+    const float *dt_bias;
+    const float *conv_w;
+    const float *norm;
+    const void *z;
+    float *out;
+    uint32_t *err_word;
+    float eps;
+    uint32_t key_heads, value_heads, conv_k, channels, max_slots;
+    int bf16_in;
+    // forces every field into a register here, so all the reads are issued
+    // together and waited for once
+    __device__ __forceinline__ void pin() {
+        state = pin_global(state);
+        history = pin_global(history);
+        qkv = pin_global(qkv);
+        a = pin_global(a);
+        b = pin_global(b);
+        a_log = pin_global(a_log);
+        dt_bias = pin_global(dt_bias);
+        conv_w = pin_global(conv_w);
+        norm = pin_global(norm);
+        z = pin_global(z);
+        out = pin_global(out);
+        err_word = pin_global(err_word);
+        asm volatile("" : "+s"(eps), "+s"(key_heads), "+s"(value_heads), "+s"(conv_k),
+                     "+s"(channels), "+s"(max_slots), "+s"(bf16_in));
+    }
+};
 constexpr int kHeadCh = 2 * kDk + kHeadDv;  // q, k and v channels of one head
 constexpr int kHeadThreads = 512;
 
@@ -269,15 +306,23 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     const int wave = tid >> 6;
     const int group = tid >> 4;
     const int l16 = tid & 15;
-    const bool bf16_in = p.bf16_in != 0;
+    // Every kernel argument used below is read here, in one batch of scalar
+    // loads with one wait: left to itself the compiler reads each just before
+    // its first use, and the state loads then sit behind several dependent
+    // scalar round trips.
+    HeadArgs a{p.state, p.history, p.qkv, p.a, p.b, p.a_log, p.dt_bias, p.conv_w, norm, z, out,
+               err_word, eps, p.key_heads, p.value_heads, p.conv_k, p.channels, p.max_slots,
+               p.bf16_in};
+    a.pin();
+    const bool bf16_in = a.bf16_in != 0;
 
-    const uint32_t h = blockIdx.x % p.value_heads;
-    const GdnMeta m = p.meta[blockIdx.x / p.value_heads];
-    const uint32_t groups = p.value_heads / p.key_heads;
+    const uint32_t h = blockIdx.x % a.value_heads;
+    const GdnMeta m = p.meta[blockIdx.x / a.value_heads];
+    const uint32_t groups = a.value_heads / a.key_heads;
     const uint32_t kh = h / groups;
-    const uint32_t key_width = p.key_heads * kDk;
-    const uint32_t K1 = p.conv_k - 1;
-    const size_t width = (size_t)p.value_heads * kHeadDv;
+    const uint32_t key_width = a.key_heads * kDk;
+    const uint32_t K1 = a.conv_k - 1;
+    const size_t width = (size_t)a.value_heads * kHeadDv;
     auto chan = [&](int c) -> uint32_t {
         if (c < kDk) return kh * kDk + c;
         if (c < 2 * kDk) return key_width + kh * kDk + (c - kDk);
@@ -289,23 +334,23 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     const uint32_t ch0 = one ? chan(tid) : 0;
     const uint32_t ch1 = two ? chan(tid + NTH) : 0;
 
-    const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
-    const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
+    const size_t hist_slot = ((size_t)m.parity * a.max_slots + m.slot) * a.channels;
+    const size_t hist_next = ((size_t)(1 - m.parity) * a.max_slots + m.slot) * a.channels;
     // (all loads unconditional: a conditional load ends in a wait for every
     // load in flight; threads without a channel read channel 0 and ignore it)
     ConvChan cv0, cv1;
-    cv0.load(p.history + (hist_slot + ch0) * K1, p.conv_w + (size_t)ch0 * p.conv_k, p.conv_k);
-    cv1.load(p.history + (hist_slot + ch1) * K1, p.conv_w + (size_t)ch1 * p.conv_k, p.conv_k);
+    cv0.load(a.history + (hist_slot + ch0) * K1, a.conv_w + (size_t)ch0 * a.conv_k, a.conv_k);
+    cv1.load(a.history + (hist_slot + ch1) * K1, a.conv_w + (size_t)ch1 * a.conv_k, a.conv_k);
     // inputs of a row: qkv channels, z of this head (dims lane and lane + 64,
     // used by wave 0), a and b
     float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f, av = 0.0f, bv = 0.0f;
     auto load_row = [&](size_t row) {
-        x0 = load_act_nb(p.qkv, row * p.channels + ch0, bf16_in);
-        x1 = load_act_nb(p.qkv, row * p.channels + ch1, bf16_in);
-        z0 = load_act_nb(z, row * width + h * kHeadDv + lane, bf16_in);
-        z1 = load_act_nb(z, row * width + h * kHeadDv + lane + 64, bf16_in);
-        av = load_act_nb(p.a, row * p.value_heads + h, bf16_in);
-        bv = load_act_nb(p.b, row * p.value_heads + h, bf16_in);
+        x0 = load_act_nb(a.qkv, row * a.channels + ch0, bf16_in);
+        x1 = load_act_nb(a.qkv, row * a.channels + ch1, bf16_in);
+        z0 = load_act_nb(a.z, row * width + h * kHeadDv + lane, bf16_in);
+        z1 = load_act_nb(a.z, row * width + h * kHeadDv + lane + 64, bf16_in);
+        av = load_act_nb(a.a, row * a.value_heads + h, bf16_in);
+        bv = load_act_nb(a.b, row * a.value_heads + h, bf16_in);
     };
     load_row(m.row0);
     // state rows v = (NTH/16) i + group, dims [4 l16, 4 l16 + 4) and
@@ -313,7 +358,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // then covers 256 contiguous bytes of a row; requested after
     // the (branchy) conv loads so that nothing waits for them before the
     // delta step itself
-    float *sbase = p.state + ((size_t)m.slot * p.value_heads + h) * kHeadDv * kDk + l16 * 4;
+    float *sbase = a.state + ((size_t)m.slot * a.value_heads + h) * kHeadDv * kDk + l16 * 4;
     // the state is read once and written once per call: nontemporal
     // accesses (streaming reads measured ~8 % faster than ordinary loads)
     typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
@@ -326,17 +371,17 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         S[i][0] = x0.x; S[i][1] = x0.y; S[i][2] = x0.z; S[i][3] = x0.w;
         S[i][4] = x1.x; S[i][5] = x1.y; S[i][6] = x1.z; S[i][7] = x1.w;
     }
-    const float a_log_e = expf(p.a_log[h]);
-    const float dt = p.dt_bias[h];
+    const float a_log_e = expf(a.a_log[h]);
+    const float dt = a.dt_bias[h];
     const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:213
-    const float nw0 = norm[lane], nw1 = norm[lane + 64];
+    const float nw0 = a.norm[lane], nw1 = a.norm[lane + 64];
     __syncthreads();
 
     for (uint32_t r = 0; r < m.rows; ++r) {
         const size_t row = (size_t)m.row0 + r;
         // A. causal conv + silu (math.rs:175-185), history in registers
-        if (one) conv_s[tid] = cv0.step(x0, p.conv_k);
-        if (two) conv_s[tid + NTH] = cv1.step(x1, p.conv_k);
+        if (one) conv_s[tid] = cv0.step(x0, a.conv_k);
+        if (two) conv_s[tid + NTH] = cv1.step(x1, a.conv_k);
         if (tid == 0) {
             // math.rs:220-221
             ab_s[0] = expf(-a_log_e * softplus_ref(av + dt));
@@ -400,9 +445,9 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
             const float o0 = out_s[lane], o1 = out_s[lane + 64];
             const float ss = sum64(o0 * o0 + o1 * o1);
             const float variance = ss / (float)kHeadDv;
-            if (!isfinite(variance) && lane == 0) atomicOr(err_word, kErrNonFiniteVariance);
-            const float inv = 1.0f / sqrtf(variance + eps);
-            float *dst = out + row * width + h * kHeadDv;
+            if (!isfinite(variance) && lane == 0) atomicOr(a.err_word, kErrNonFiniteVariance);
+            const float inv = 1.0f / sqrtf(variance + a.eps);
+            float *dst = a.out + row * width + h * kHeadDv;
             dst[lane] = o0 * inv * nw0 * (zc0 * ref_sigmoid(zc0));
             dst[lane + 64] = o1 * inv * nw1 * (zc1 * ref_sigmoid(zc1));
         }
@@ -411,8 +456,8 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // next history: v channels here; q/k channels by the first value head of
     // the key group (the others compute the same values)
     const bool owns_qk = (h % groups == 0);
-    if (one && (tid >= 2 * kDk || owns_qk)) cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
-    if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(p.history + (hist_next + ch1) * K1, p.conv_k);
+    if (one && (tid >= 2 * kDk || owns_qk)) cv0.store(a.history + (hist_next + ch0) * K1, a.conv_k);
+    if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(a.history + (hist_next + ch1) * K1, a.conv_k);
 }
 
 // ---------------------------------------------------------------------------

@@ -61,6 +61,18 @@ __device__ __forceinline__ int wave_index() {
     return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// Pins a kernel-argument pointer in scalar registers at this point (its read
+// is issued with the other argument reads and waited for once, not at each
+// first use) and hands it back as a pointer still known to address global
+// memory: a pointer pinned as is becomes generic, and loads through it flat
+// loads, which also count against the LDS wait counter.
+template <typename T>
+__device__ __forceinline__ T *pin_global(T *p) {
+    uint64_t v = (uint64_t)p;
+    asm volatile("" : "+s"(v));
+    return (T *)(__attribute__((address_space(1))) T *)v;
+}
+
 // DPP controls (gfx9 encoding): quad permutes, half-row and row mirrors.
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
