@@ -291,7 +291,7 @@ struct HeadArgs {
 constexpr int kHeadCh = 2 * kDk + kHeadDv;  // q, k and v channels of one head
 constexpr int kHeadThreads = 512;
 
-template <int NTH>
+template <int NTH, class Conv>
 __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const float *norm,
                                                             const void *z, float *out,
                                                             uint32_t *err_word, float eps) {
@@ -310,14 +310,16 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // loads with one wait: left to itself the compiler reads each just before
     // its first use, and the state loads then sit behind several dependent
     // scalar round trips.
+    // grid (value head, sequence): the sequence's entry needs no argument
+    // to locate it, so it is read in the same batch
+    const GdnMeta m = p.meta[blockIdx.y];
     HeadArgs a{p.state, p.history, p.qkv, p.a, p.b, p.a_log, p.dt_bias, p.conv_w, norm, z, out,
                err_word, eps, p.key_heads, p.value_heads, p.conv_k, p.channels, p.max_slots,
                p.bf16_in};
     a.pin();
     const bool bf16_in = a.bf16_in != 0;
 
-    const uint32_t h = blockIdx.x % a.value_heads;
-    const GdnMeta m = p.meta[blockIdx.x / a.value_heads];
+    const uint32_t h = blockIdx.x;
     const uint32_t groups = a.value_heads / a.key_heads;
     const uint32_t kh = h / groups;
     const uint32_t key_width = a.key_heads * kDk;
@@ -328,9 +330,11 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         if (c < 2 * kDk) return key_width + kh * kDk + (c - kDk);
         return 2 * key_width + h * kHeadDv + (c - 2 * kDk);
     };
-    // this thread's conv channels: tid (if < 384), and tid + NTH when that is < 384
+    // this thread's conv channels: tid (if < 384), and tid + NTH when that is
+    // < 384 (only with fewer than 384 threads)
+    constexpr bool kTwo = NTH < kHeadCh;
     const bool one = tid < kHeadCh;
-    const bool two = tid + NTH < kHeadCh;
+    const bool two = kTwo && tid + NTH < kHeadCh;
     const uint32_t ch0 = one ? chan(tid) : 0;
     const uint32_t ch1 = two ? chan(tid + NTH) : 0;
 
@@ -338,15 +342,17 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     const size_t hist_next = ((size_t)(1 - m.parity) * a.max_slots + m.slot) * a.channels;
     // (all loads unconditional: a conditional load ends in a wait for every
     // load in flight; threads without a channel read channel 0 and ignore it)
-    ConvChan cv0, cv1;
+    Conv cv0, cv1;
     cv0.load(a.history + (hist_slot + ch0) * K1, a.conv_w + (size_t)ch0 * a.conv_k, a.conv_k);
-    cv1.load(a.history + (hist_slot + ch1) * K1, a.conv_w + (size_t)ch1 * a.conv_k, a.conv_k);
+    if constexpr (kTwo) {
+        cv1.load(a.history + (hist_slot + ch1) * K1, a.conv_w + (size_t)ch1 * a.conv_k, a.conv_k);
+    }
     // inputs of a row: qkv channels, z of this head (dims lane and lane + 64,
     // used by wave 0), a and b
     float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f, av = 0.0f, bv = 0.0f;
     auto load_row = [&](size_t row) {
         x0 = load_act_nb(a.qkv, row * a.channels + ch0, bf16_in);
-        x1 = load_act_nb(a.qkv, row * a.channels + ch1, bf16_in);
+        if constexpr (kTwo) x1 = load_act_nb(a.qkv, row * a.channels + ch1, bf16_in);
         z0 = load_act_nb(a.z, row * width + h * kHeadDv + lane, bf16_in);
         z1 = load_act_nb(a.z, row * width + h * kHeadDv + lane + 64, bf16_in);
         av = load_act_nb(a.a, row * a.value_heads + h, bf16_in);
@@ -381,7 +387,9 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         const size_t row = (size_t)m.row0 + r;
         // A. causal conv + silu (math.rs:175-185), history in registers
         if (one) conv_s[tid] = cv0.step(x0, a.conv_k);
-        if (two) conv_s[tid + NTH] = cv1.step(x1, a.conv_k);
+        if constexpr (kTwo) {
+            if (two) conv_s[tid + NTH] = cv1.step(x1, a.conv_k);
+        }
         if (tid == 0) {
             // math.rs:220-221
             ab_s[0] = expf(-a_log_e * softplus_ref(av + dt));
@@ -457,7 +465,9 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // the key group (the others compute the same values)
     const bool owns_qk = (h % groups == 0);
     if (one && (tid >= 2 * kDk || owns_qk)) cv0.store(a.history + (hist_next + ch0) * K1, a.conv_k);
-    if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(a.history + (hist_next + ch1) * K1, a.conv_k);
+    if constexpr (kTwo) {
+        if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(a.history + (hist_next + ch1) * K1, a.conv_k);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -589,6 +599,10 @@ struct ConvK {
         for (int j = 0; j + 1 < K - 1; ++j) hist[j] = hist[j + 1];
         if constexpr (K > 1) hist[K - 2] = x;
         return value;
+    }
+    __device__ __forceinline__ float step(float x, uint32_t K_) {
+        const float value = pre(x, K_);
+        return value * ref_sigmoid(value);
     }
     __device__ __forceinline__ void store(float *history_row, uint32_t) const {
 #pragma unroll
@@ -1143,9 +1157,15 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
             p.meta[i] = GdnMeta{slots[base + i], rows[base + i], row0[base + i], parity[base + i]};
         }
         if (head_kernel) {
-            const uint32_t blocks = (uint32_t)n * pool->value_heads;
-            hipLaunchKernelGGL(gdn_head_kernel<kHeadThreads>, dim3(blocks), dim3(kHeadThreads), 0,
-                               stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
+            const dim3 grid(pool->value_heads, (uint32_t)n);
+            if (p.conv_k == 4) {
+                hipLaunchKernelGGL((gdn_head_kernel<kHeadThreads, ConvK<4>>), grid, dim3(kHeadThreads),
+                                   0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
+            } else {
+                hipLaunchKernelGGL((gdn_head_kernel<kHeadThreads, ConvChan>), grid,
+                                   dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word,
+                                   g.eps);
+            }
         } else if (chunk_kernel) {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kVs);
             const hipError_t e = p.conv_k == 4 ? launch_chunk<ConvK<4>>(stream, p, blocks)

@@ -196,6 +196,25 @@ def test_gdn_chunked_form_ragged_rows_seeded_state(pkg, backend, rng):
     pool.destroy()
 
 
+def test_gdn_decode_kernel_conv_sizes(pkg, backend, rng):
+    # decode-sized calls (at most 8 rows per sequence, Dv 128) with conv
+    # kernels other than 4 (run-time taps) and 4 itself (compile-time taps),
+    # over two calls so the history carries: outputs, states, histories
+    for hk, hv, K in ((2, 8, 1), (1, 4, 3), (2, 4, 6), (4, 8, 4)):
+        L = Layer(rng, hk, hv, 128, 128, K)
+        pool = pkg.GdnState(backend, hk, hv, 128, 128, K, 3)
+        seqs, refs = [], []
+        for _ in range(3):
+            s = pool.open()
+            m, h = seeded_state(rng, L)
+            pool.write(s, m, h)
+            seqs.append(s)
+            refs.append((m.copy(), h.copy()))
+        for call, rows in enumerate(([1, 8, 3], [2, 1, 1])):
+            run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, f"hk {hk} hv {hv} K {K} call {call}")
+        pool.destroy()
+
+
 def test_gdn_chunked_form_key_groups_and_conv_sizes(pkg, backend, rng):
     # key groups of 1 and 4, conv kernels 1 (no history), 2 and 6
     for hk, hv, K in ((4, 4, 1), (1, 4, 2), (2, 8, 6)):
