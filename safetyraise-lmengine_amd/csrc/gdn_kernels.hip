@@ -1102,6 +1102,35 @@ __global__ void __launch_bounds__(256) gdn_norm_gate_kernel(const NormParams p) 
     const int lane = threadIdx.x & 63;
     if (wid >= p.rows * p.value_heads) return;
     const size_t base = (size_t)wid * p.value_dim;
+    if (p.value_dim <= 4 * 64) {
+        // every input of the row (raw, z, weights) is requested before the
+        // reduction, so the kernel waits for one memory round trip, not two;
+        // loads past value_dim read its last element and are not used
+        const bool bf16_in = p.bf16_in != 0;
+        float x[4], zz[4], nw[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = min((uint32_t)lane + 64 * i, p.value_dim - 1);
+            x[i] = p.raw[base + d];
+            zz[i] = load_act_nb(p.z, base + d, bf16_in);
+            nw[i] = p.norm[d];
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if ((uint32_t)lane + 64 * i < p.value_dim) ss += x[i] * x[i];
+        }
+        ss = sum64(ss);
+        const float variance = ss / (float)p.value_dim;
+        if (!isfinite(variance) && lane == 0) atomicOr(p.err_word, kErrNonFiniteVariance);
+        const float inv = 1.0f / sqrtf(variance + p.eps);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d = (uint32_t)lane + 64 * i;
+            if (d < p.value_dim) p.out[base + d] = x[i] * inv * nw[i] * (zz[i] * ref_sigmoid(zz[i]));
+        }
+        return;
+    }
     float ss = 0.0f;
     for (uint32_t d = lane; d < p.value_dim; d += 64) {
         const float x = p.raw[base + d];
