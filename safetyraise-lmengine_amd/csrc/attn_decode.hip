@@ -643,12 +643,14 @@ __global__ void __launch_bounds__(kThreads) attn_decode_kernel(const DecodeParam
 }
 
 // Merges the per-segment (max, sum, output) records of every sequence that
-// has more than one, one workgroup per (sequence, KV head), in one pass with
-// a running rescale, and applies the output gate.  It runs after
-// attn_decode_kernel on the same stream, so the kernel boundary orders the
-// records before they are read (no device-scope fences).
+// has more than one in one pass with a running rescale, and applies the
+// output gate: one workgroup per (sequence, KV head) x query head of the
+// group, one thread per output dim, so each thread's record loads are all in
+// flight together.  It runs after attn_decode_kernel on the same stream, so
+// the kernel boundary orders the records before they are read (no
+// device-scope fences).
 template <int D, int G>
-__global__ void __launch_bounds__(kThreads) attn_combine_kernel(const DecodeParams p) {
+__global__ void __launch_bounds__(D) attn_combine_kernel(const DecodeParams p) {
     const uint32_t kvh = blockIdx.x % p.kv_heads;
     const uint32_t s = blockIdx.x / p.kv_heads;
     const uint32_t nrec = p.meta[s].nrec;
@@ -664,9 +666,9 @@ __global__ void __launch_bounds__(kThreads) attn_combine_kernel(const DecodePara
     const float *recs = p.partials + ((size_t)p.meta[s].rec0 * p.kv_heads + kvh) * G * (D + 2);
     const size_t rec_stride = (size_t)p.kv_heads * G * (D + 2);  // between records
     constexpr uint32_t kBatch = 8;  // independent loads in flight per thread
-    for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
-        const int h = idx / D;
-        const int d = idx - h * D;
+    {
+        const int h = blockIdx.y;
+        const int d = threadIdx.x;
         const float *r0 = recs + (size_t)h * (D + 2);
         float M = -INFINITY, L = 0.0f, O = 0.0f;
         for (uint32_t sp = 0; sp < nrec; sp += kBatch) {
@@ -743,8 +745,8 @@ hipError_t launch_dgp(hipStream_t stream, DecodeParams &prm, const DecodePlanInp
     if (e != hipSuccess || recs == prm.nseq) {
         return e;  // every sequence in one segment: nothing to combine
     }
-    hipLaunchKernelGGL((attn_combine_kernel<D, G>), dim3(prm.nseq * prm.kv_heads), dim3(kThreads),
-                       0, stream, prm);
+    hipLaunchKernelGGL((attn_combine_kernel<D, G>), dim3(prm.nseq * prm.kv_heads, G), dim3(D), 0,
+                       stream, prm);
     return hipGetLastError();
 }
 
