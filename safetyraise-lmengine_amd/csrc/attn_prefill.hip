@@ -1611,13 +1611,21 @@ attn_verify_kernel(const VerifyParams vp) {
         }
 }
 
-// One wave per (sequence, row, head): merges the partition records in the
-// log2 domain, divides by the sum, applies the Qwen3.5 gate and stores.
+// One workgroup of four waves per (sequence, row, head): merges the
+// partition records in the log2 domain, divides by the sum, applies the
+// Qwen3.5 gate and stores.  Wave w takes records w, w + 4, ...; every record
+// load of a batch is in flight at once, and the four partial sums meet in LDS.
+constexpr int kCombineWaves = 4;
+
 template <int D>
-__global__ __launch_bounds__(256) void attn_verify_combine_kernel(const VerifyParams vp) {
+__global__ __launch_bounds__(64 * kCombineWaves) void attn_verify_combine_kernel(const VerifyParams vp) {
     constexpr int EPL = D / 64;
+    constexpr int kUnroll = 8;  // records per batch of loads
+    __shared__ float part_s[kCombineWaves][D + 1];
+    __shared__ float max_s[kCombineWaves];
     const PrefillParams &p = vp.p;
-    const uint32_t w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t w = blockIdx.x;
+    const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     uint32_t s = 0, base = 0;
     for (; s < p.nseq; ++s) {
@@ -1625,43 +1633,62 @@ __global__ __launch_bounds__(256) void attn_verify_combine_kernel(const VerifyPa
         if (w < base + n) break;
         base += n;
     }
-    if (s >= p.nseq) return;
+    if (s >= p.nseq) return;  // whole workgroup: no barrier is skipped by part of it
     const PrefillMeta m = p.meta[s];
     const uint32_t r = (w - base) / p.heads;
     const uint32_t head = (w - base) % p.heads;
     const uint32_t nparts = m.nblk;
     const float *rec = vp.partials +
                        ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nparts) * kRecordStride<D>;
-    // partition maxima, 64 partitions per pass across the lanes
+    // maximum over the partition maxima, all threads of the workgroup
     float mx = -INFINITY;
-    for (uint32_t q = lane; q < nparts; q += 64) mx = fmaxf(mx, rec[(size_t)q * kRecordStride<D>]);
+    for (uint32_t q = threadIdx.x; q < nparts; q += 64 * kCombineWaves) {
+        mx = fmaxf(mx, rec[(size_t)q * kRecordStride<D>]);
+    }
     mx = max64(mx);
+    if (lane == 0) max_s[wave] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kCombineWaves; ++i) mx = fmaxf(mx, max_s[i]);
+    // this wave's records: weight 2^(m - max) (0 for a record with no
+    // visible key, m = -inf, whose o is never used), sum and output
     float l = 0.0f;
     float o[EPL] = {};
-    for (uint32_t q0 = 0; q0 < nparts; q0 += 64) {
-        // lane j holds the weight of partition q0 + j; a partition with no
-        // visible key (m = -inf) has weight 0 and its o is never read
-        float sc = 0.0f;
-        if (q0 + lane < nparts) {
-            const float2 ml = *(const float2 *)(rec + (size_t)(q0 + lane) * kRecordStride<D>);
-            if (ml.x != -INFINITY) {
-                sc = fast_exp2(ml.x - mx);
-                l += ml.y * sc;
-            }
-        }
-        const uint32_t n = min(64u, nparts - q0);
-#pragma unroll 4
-        for (uint32_t j = 0; j < n; ++j) {
-            const float w = __shfl(sc, (int)j);
-            const float *rq = rec + (size_t)(q0 + j) * kRecordStride<D> + 4;
+    for (uint32_t q0 = wave; q0 < nparts; q0 += kCombineWaves * kUnroll) {
+        float2 ml[kUnroll];
+        float x[kUnroll][EPL];
 #pragma unroll
-            for (int i = 0; i < EPL; ++i) {
-                const float x = rq[lane + 64 * i];
-                o[i] += w != 0.0f ? x * w : 0.0f;
-            }
+        for (int u = 0; u < kUnroll; ++u) {
+            // past the last record: the last one again, with weight 0
+            const uint32_t q = min(q0 + (uint32_t)(kCombineWaves * u), nparts - 1);
+            const float *rq = rec + (size_t)q * kRecordStride<D>;
+            ml[u] = *(const float2 *)rq;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) x[u][i] = rq[4 + lane + 64 * i];
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const bool live = q0 + (uint32_t)(kCombineWaves * u) < nparts && ml[u].x != -INFINITY;
+            const float sc = live ? fast_exp2(ml[u].x - mx) : 0.0f;
+            l += live ? ml[u].y * sc : 0.0f;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) o[i] += live ? x[u][i] * sc : 0.0f;
         }
     }
-    l = sum64(l);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) part_s[wave][lane + 64 * i] = o[i];
+    if (lane == 0) part_s[wave][D] = l;
+    __syncthreads();
+    if (wave != 0) return;
+    l = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kCombineWaves; ++k) l += part_s[k][D];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        o[i] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kCombineWaves; ++k) o[i] += part_s[k][lane + 64 * i];
+    }
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
     const uint32_t hs = gated ? 2 * D : D;
@@ -1681,7 +1708,7 @@ __global__ __launch_bounds__(256) void attn_verify_combine_kernel(const VerifyPa
 
 template <int D>
 hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
-                           uint32_t combine_waves) {
+                           uint32_t combine_rows) {
     static bool configured = false;
     const size_t lds = 8 * kTileBytes<D> + kVerifyPageSlots * sizeof(int32_t);
     if (!configured) {
@@ -1695,8 +1722,8 @@ hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t 
                        vp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_verify_combine_kernel<D>, dim3((combine_waves + 3) / 4), dim3(256), 0,
-                       stream, vp);
+    hipLaunchKernelGGL(attn_verify_combine_kernel<D>, dim3(combine_rows), dim3(64 * kCombineWaves),
+                       0, stream, vp);
     return hipGetLastError();
 }
 
