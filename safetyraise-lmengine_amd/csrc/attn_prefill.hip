@@ -206,7 +206,7 @@ __device__ __forceinline__ void store_span_bf16(uint16_t *base, size_t i, const 
     }
 }
 
-template <int D>
+template <int D, bool kBf16In>
 __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams p) {
     constexpr int EPL = D / 16;
     constexpr int HW = kAppendHeadsPerWave;
@@ -219,6 +219,27 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     const int slot = lane >> 4;  // head of the wave this lane works on
     const int l16 = lane & 15;
     const PrefillMeta m = p.meta[blockIdx.y];
+    // the kernel arguments used below, read in one batch and waited for once
+    // (left to itself the compiler reads each just before its first use,
+    // several dependent scalar round trips ahead of the first vector load)
+    uint64_t bk = (uint64_t)p.k, bv = (uint64_t)p.v, bkn = (uint64_t)p.k_norm,
+             bpt = (uint64_t)p.page_table, bpos = (uint64_t)p.positions, bcs = (uint64_t)p.rope_cs,
+             berr = (uint64_t)p.err_word, bkp = (uint64_t)p.k_pages, bvp = (uint64_t)p.v_pages;
+    uint32_t kv_heads = p.kv_heads, flags = p.flags, pages_per_seq = p.pages_per_seq,
+             lpt = p.log2_page_tokens, rotary_dim = p.rotary_dim, num_pages = p.num_pages;
+    float eps = p.eps;
+    asm volatile("" : "+s"(bk), "+s"(bv), "+s"(bkn), "+s"(bpt), "+s"(bpos), "+s"(bcs), "+s"(berr),
+                 "+s"(bkp), "+s"(bvp), "+s"(kv_heads), "+s"(flags), "+s"(pages_per_seq), "+s"(lpt),
+                 "+s"(rotary_dim), "+s"(num_pages), "+s"(eps));
+    const void *k_in = global_from_bits<const void>(bk);
+    const void *v_in = global_from_bits<const void>(bv);
+    const float *k_norm = global_from_bits<const float>(bkn);
+    const int32_t *page_table = global_from_bits<const int32_t>(bpt);
+    const int32_t *positions = global_from_bits<const int32_t>(bpos);
+    float2 *rope_cs = global_from_bits<float2>(bcs);
+    uint32_t *err_word = global_from_bits<uint32_t>(berr);
+    uint16_t *k_pages = global_from_bits<uint16_t>(bkp);
+    uint16_t *v_pages = global_from_bits<uint16_t>(bvp);
     // entries of this call's page-table update: block (0,0) writes them for
     // the kernels that follow; every row takes its own page from the list
     // (the table itself may not hold it yet)
@@ -228,50 +249,65 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
         }
     }
     // no barrier below, so a wave past the rows just ends
-    const uint32_t quads = (p.kv_heads + HW - 1) / HW;
+    const uint32_t quads = (kv_heads + HW - 1) / HW;
     const uint32_t w = blockIdx.x * 4 + wave;
     const uint32_t r = w / quads;
     const uint32_t quad = w - r * quads;
     if (r >= m.rows) return;
     const uint32_t row = m.row0 + r;
-    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
-    const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
-    const bool interleaved = (p.flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
-    const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
+    // the input type is a template parameter: a run-time branch around the
+    // span loads would end each in a wait for every load in flight
+    constexpr bool bf16_in = kBf16In;
+    const bool qk_norm = (flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
+    const bool interleaved = (flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
+    const float norm_add = (flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
 
     const uint32_t kvh_raw = quad * HW + slot;
-    const bool head_ok = kvh_raw < p.kv_heads;
-    const uint32_t kvh = min(kvh_raw, p.kv_heads - 1);  // lanes past the heads repeat the last
+    const bool head_ok = kvh_raw < kv_heads;
+    const uint32_t kvh = min(kvh_raw, kv_heads - 1);  // lanes past the heads repeat the last
     const uint32_t e0 = l16 * EPL;                     // first element of this lane
-    const size_t src = ((size_t)row * p.kv_heads + kvh) * D + e0;
+    const size_t src = ((size_t)row * kv_heads + kvh) * D + e0;
     float x[EPL], vv[EPL], wk[EPL];
-    load_span<EPL>(p.k, src, bf16_in, x);
-    load_span<EPL>(p.v, src, bf16_in, vv);
-    load_span<EPL>(p.k_norm, e0, false, wk);  // readable without QK-norm too
+    load_span<EPL>(k_in, src, bf16_in, x);
+    load_span<EPL>(v_in, src, bf16_in, vv);
+    load_span<EPL>(k_norm, e0, false, wk);  // readable without QK-norm too
 
     const uint32_t tok = m.ctx + r;
-    const uint32_t tidx = m.slot * p.pages_per_seq + (tok >> p.log2_page_tokens);
-    int32_t page = p.page_table[tidx];
+    const uint32_t tidx = m.slot * pages_per_seq + (tok >> lpt);
+    int32_t page = page_table[tidx];
+    // the RoPE table's inputs (the row's three position axes, this lane's
+    // frequency denominators) are requested before the first wait below, so
+    // the wave waits for one memory round trip
+    const uint32_t half = rotary_dim / 2;
+    constexpr int NTAB = (D / 2 + 63) / 64;  // table entries per lane
+    const int32_t *pos3 = positions + (size_t)row * 3;
+    const int32_t pz0 = pos3[0], pz1 = pos3[1], pz2 = pos3[2];
+    float den[NTAB];
+#pragma unroll
+    for (int k = 0; k < NTAB; ++k) den[k] = p.rope.denom[min((uint32_t)lane + 64 * k, half - 1)];
     {
         const bool hit = (uint32_t)lane < p.tbl_n && p.tbl_idx[min((uint32_t)lane, kInlineTable - 1)] == tidx;
         const uint64_t mask = __builtin_amdgcn_ballot_w64(hit);
         if (mask != 0) page = p.tbl_val[__builtin_ctzll(mask)];
     }
-    const uint32_t pt_mask = (1u << p.log2_page_tokens) - 1;
-    const uint32_t half = p.rotary_dim / 2;
+    const uint32_t pt_mask = (1u << lpt) - 1;
 
     // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with an IEEE
     // f32 division (math.rs:90-91); each wave of the row computes the row's
     // table, the first also saves it for the q side
-    const int32_t *pos3 = p.positions + (size_t)row * 3;
-    for (uint32_t i = lane; i < half; i += 64) {
-        const int axis = rope_axis(i, p.mrope, interleaved);
-        const float angle = (float)pos3[axis] / p.rope.denom[i];
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        cs_s[wave][i] = cs;
-        sn_s[wave][i] = sn;
-        if (quad == 0) p.rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
+#pragma unroll
+    for (int k = 0; k < NTAB; ++k) {
+        const uint32_t i = lane + 64 * k;
+        if (i < half) {
+            const int axis = rope_axis(i, p.mrope, interleaved);
+            const int32_t pos = axis == 0 ? pz0 : axis == 1 ? pz1 : pz2;
+            const float angle = (float)pos / den[k];
+            float sn, cs;
+            sincosf(angle, &sn, &cs);
+            cs_s[wave][i] = cs;
+            sn_s[wave][i] = sn;
+            if (quad == 0) rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
+        }
     }
     if (qk_norm) {
         // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
@@ -280,8 +316,8 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
         for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
         ss = sum16(ss);
         const float variance = ss / (float)D;
-        if (!isfinite(variance) && l16 == 0 && head_ok) atomicOr(p.err_word, kErrNonFiniteVariance);
-        const float inv = 1.0f / sqrtf(variance + p.eps);
+        if (!isfinite(variance) && l16 == 0 && head_ok) atomicOr(err_word, kErrNonFiniteVariance);
+        const float inv = 1.0f / sqrtf(variance + eps);
 #pragma unroll
         for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (wk[i] + norm_add);
     }
@@ -301,7 +337,7 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     for (int i = 0; i < EPL; ++i) {
         const uint32_t e = e0 + i;
         y[i] = x[i];
-        if (e < p.rotary_dim) {
+        if (e < rotary_dim) {
             const bool lo = e < half;
             const uint32_t pi = lo ? e : e - half;
             const float partner = xs[wave][slot][lo ? e + half : e - half];
@@ -313,12 +349,12 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
 #pragma unroll
     for (int i = 0; i < EPL; ++i) finite = finite && isfinite(y[i]) && isfinite(vv[i]);
     if (head_ok) {
-        const size_t dst = ((((size_t)kvh * p.num_pages + page) << p.log2_page_tokens) + (tok & pt_mask)) * D + e0;
-        store_span_bf16<EPL>(p.k_pages, dst, y);
-        store_span_bf16<EPL>(p.v_pages, dst, vv);
+        const size_t dst = ((((size_t)kvh * num_pages + page) << lpt) + (tok & pt_mask)) * D + e0;
+        store_span_bf16<EPL>(k_pages, dst, y);
+        store_span_bf16<EPL>(v_pages, dst, vv);
     }
     if (__builtin_amdgcn_ballot_w64(head_ok && !finite) != 0 && lane == 0) {
-        atomicOr(p.err_word, kErrNonFiniteKv);
+        atomicOr(err_word, kErrNonFiniteKv);
     }
 }
 
@@ -327,7 +363,12 @@ template <int D>
 void launch_append(hipStream_t stream, const PrefillParams &p, uint32_t max_rows) {
     const uint32_t quads = (p.kv_heads + kAppendHeadsPerWave - 1) / kAppendHeadsPerWave;
     const uint32_t waves = max_rows * quads;
-    hipLaunchKernelGGL(kv_append_rows_kernel<D>, dim3((waves + 3) / 4, p.nseq), dim3(256), 0, stream, p);
+    const dim3 grid((waves + 3) / 4, p.nseq);
+    if (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) {
+        hipLaunchKernelGGL((kv_append_rows_kernel<D, true>), grid, dim3(256), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((kv_append_rows_kernel<D, false>), grid, dim3(256), 0, stream, p);
+    }
 }
 
 // ---------------------------------------------------------------------------

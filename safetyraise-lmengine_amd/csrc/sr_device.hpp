@@ -73,6 +73,14 @@ __device__ __forceinline__ T *pin_global(T *p) {
     return (T *)(__attribute__((address_space(1))) T *)v;
 }
 
+// A pointer held as an integer (for example pinned together with other
+// values in one asm statement), back as a pointer known to address global
+// memory.
+template <typename T>
+__device__ __forceinline__ T *global_from_bits(uint64_t v) {
+    return (T *)(__attribute__((address_space(1))) T *)v;
+}
+
 // DPP controls (gfx9 encoding): quad permutes, half-row and row mirrors.
 constexpr int kDppQuadXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;   // quad_perm [2,3,0,1]
