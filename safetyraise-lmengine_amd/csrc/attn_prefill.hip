@@ -724,9 +724,23 @@ __device__ __forceinline__ QArgs q_args(const PrefillParams &p) {
     return a;
 }
 
-template <int D>
+// The row's RoPE (cos, sin) pairs read from global memory (rope_cs), or from
+// a copy of the workgroup's rows in LDS (LdsRope).
+struct GlobalRope {
+    const float2 *row;
+    __device__ __forceinline__ f32x4 pairs(uint32_t i) const { return *(const f32x4 *)(row + i); }
+};
+struct LdsRope {
+    const __attribute__((address_space(3))) float2 *row;
+    __device__ __forceinline__ f32x4 pairs(uint32_t i) const {
+        return *(const __attribute__((address_space(3))) f32x4 *)(row + i);
+    }
+};
+
+template <int D, class Rope = GlobalRope>
 __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_t call_row,
-                                           int h, int lane, f16x8 (&qop)[D / 16]) {
+                                           int h, int lane, f16x8 (&qop)[D / 16],
+                                           const Rope *rope = nullptr) {
     constexpr int NS = D / 16;
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
@@ -738,7 +752,9 @@ __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_
     // multiple of 32, here) and q itself.
     const uint32_t half = p.rotary_dim / 2;
     const uint32_t hsteps = p.rotary_dim / 32;
-    const float2 *cs_row = p.rope_cs + (size_t)call_row * half;
+    Rope cs;
+    if constexpr (std::is_same<Rope, GlobalRope>::value) cs.row = p.rope_cs + (size_t)call_row * half;
+    else cs = *rope;
     f32x4 gw[NS][2];
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
@@ -748,9 +764,9 @@ __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_
     f32x4 csv[NS / 2][4];
 #pragma unroll
     for (int st = 0; st < NS / 2; ++st) {
-        const f32x4 *c4 = (const f32x4 *)(cs_row + 16 * min((uint32_t)st, hsteps - 1) + 8 * h);
+        const uint32_t c0 = 16 * min((uint32_t)st, hsteps - 1) + 8 * h;
 #pragma unroll
-        for (int j2 = 0; j2 < 4; ++j2) csv[st][j2] = c4[j2];  // (cos, sin) of pairs 2 j2, 2 j2 + 1
+        for (int j2 = 0; j2 < 4; ++j2) csv[st][j2] = cs.pairs(c0 + 2 * j2);  // pairs 2 j2, 2 j2 + 1
     }
     float x[NS][8];
     if (bf16_in) {
@@ -1167,6 +1183,19 @@ __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1))) void attn_prefill_kernel(
 template <int D>
 constexpr size_t kPingPongLds = 4 * kTileBytes<D>;  // K x 2, V x 2
 
+// The workgroup's rows' RoPE (cos, sin) pairs, staged once in LDS behind the
+// tiles for the q prologue: each row's table is read by the G waves of its
+// heads, and read from global memory each lane's 32 pairs cost 16 loads that
+// touch 32 rows each.  Rows are padded by 16 bytes so that the 32 rows of a
+// read spread over the banks.  With G = 1 a workgroup has 256 rows, too many
+// to stage: its waves read global memory.
+template <int D, int G>
+constexpr bool kStageRope = G >= 2;
+template <int D>
+constexpr uint32_t kRopePitch = D / 2 + 2;  // float2 per staged row
+template <int D, int G>
+constexpr size_t kRopeStageBytes = kStageRope<D, G> ? (size_t)2 * kRowTile * (4 / G) * kRopePitch<D> * 8 : 0;
+
 template <int D, int G, bool kTilePage>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void
 attn_prefill_pp_kernel(const PrefillParams p) {
@@ -1217,7 +1246,38 @@ attn_prefill_pp_kernel(const PrefillParams p) {
         io.load_kv(stage1, min(1u, n - 1), tb1, gt0, grp != 0);
     }
     f16x8 qop[NS];
-    q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
+    if constexpr (kStageRope<D, G>) {
+        // every load of the copy is issued before any store (indices clamped
+        // into the table; rows past the call's repeat its last row)
+        typedef __attribute__((address_space(3))) float2 lds_float2;
+        lds_float2 *rs = (lds_float2 *)(lds + kPingPongLds<D>);
+        constexpr uint32_t kRows = 2 * kRowTile * RG;
+        constexpr uint32_t kChunks = kRows * (D / 4);  // 16-byte chunks at full rotary
+        constexpr uint32_t kPer = kChunks / 512;
+        static_assert(kChunks % 512 == 0, "chunks per thread");
+        const uint32_t cpr = qa.rotary_dim / 4;  // chunks per row
+        f32x4 cv[kPer];
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = min((uint32_t)tid + 512 * u, kRows * cpr - 1);
+            const uint32_t rr = c / cpr, k = c - rr * cpr;
+            const uint32_t call_row = b.m.row0 + min(b.row0 + rr, b.m.rows - 1);
+            cv[u] = *(const f32x4 *)(qa.rope_cs + (size_t)call_row * (qa.rotary_dim / 2) + 2 * k);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = tid + 512 * u;
+            if (c < kRows * cpr) {
+                const uint32_t rr = c / cpr, k = c - rr * cpr;
+                *(__attribute__((address_space(3))) f32x4 *)(rs + rr * kRopePitch<D> + 2 * k) = cv[u];
+            }
+        }
+        __syncthreads();
+        const LdsRope rope{rs + (my_row - b.row0) * kRopePitch<D>};
+        q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop, &rope);
+    } else {
+        q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
+    }
     if (grp == 0) io.store_k(stage0, kbuf, gt0);
     else io.store_v_rows(stage0, vbuf, b.n_keys, gt0);
     uint32_t voff[NT];
@@ -1300,7 +1360,7 @@ template <int D, int G, bool kTilePage>
 hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t blocks) {
     static bool configured = false;
     if constexpr (kUsePingPong<D, G>) {
-        const size_t lds = kPingPongLds<D>;
+        const size_t lds = kPingPongLds<D> + kRopeStageBytes<D, G>;
         if (!configured) {
             const hipError_t e =
                 hipFuncSetAttribute((const void *)attn_prefill_pp_kernel<D, G, kTilePage>,

@@ -68,6 +68,19 @@ def test_prefill_gqa_group_sizes(pkg, backend, rng, heads, kv_heads):
     pool.destroy()
 
 
+@pytest.mark.parametrize("heads,kv_heads,rotary", [(16, 8, 64), (32, 8, 96), (16, 4, 32)])
+def test_prefill_partial_rotary_group_sizes(pkg, backend, rng, heads, kv_heads, rotary):
+    # head_dim 128 with partial rotary (math.rs:52-99: dims past rotary_dim
+    # unrotated) for G = 2 and 4, where the workgroup's RoPE table is staged
+    # in LDS for the q side
+    pool = new_pool(pkg, backend, kv_heads, 128, max_tokens=1024, seqs=2)
+    gq, gk = gammas(rng, 128)
+    cases = [Case(rng, pool, heads, kv_heads, 128, ctx=77, rows=150),
+             Case(rng, pool, heads, kv_heads, 128, ctx=300, rows=33)]
+    run_case(pkg, backend, pool, cases, rotary=rotary, gq=gq, gk=gk)
+    pool.destroy()
+
+
 def test_qwen2_shape_prefill_without_qk_norm(pkg, backend, rng):
     # Qwen2-0.5B attention: 14 Q / 2 KV heads (G = 7), head_dim 64, no QK-norm
     pool = new_pool(pkg, backend, 2, 64, page_tokens=32, max_tokens=1024, seqs=2)
