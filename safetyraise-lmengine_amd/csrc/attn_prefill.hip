@@ -1454,12 +1454,15 @@ constexpr int kRecordStride = D + 4;  // m, l, 2 unused, o[D] (16-byte aligned)
 // that a partition never spans more pages)
 constexpr uint32_t kVerifyPageSlots = 2048;
 
-// Tile staging of the verify producers (128 lanes, lane gt): the same LDS
-// images as TileIo (fp16 K rows with k_swz, V^T with vt_swz), but every
-// offset is recomputed from gt at each use, so that only the tiles in flight
-// occupy registers.  Page ids come from the partition's LDS copy.
+// Tile staging of the verify producers (128 lanes, lane gt): fp16 K rows with
+// k_swz; V as fp16 rows with v_swz (kRowV: D = 128, read back with
+// transposing LDS loads, so staging V costs no more than staging K) or as V^T
+// with vt_swz (D = 64).  Every offset is recomputed from gt at each use, so
+// that only the tiles in flight occupy registers.  Page ids come from the
+// partition's LDS copy.
 template <int D>
 struct VerifyIo {
+    static constexpr bool kRowV = D == 128;
     static constexpr int KCH = D / 8;                       // 16-byte chunks per row
     static constexpr int KSTEP = 128 / KCH;                 // keys per pass of the lanes
     static constexpr int KL = kKeyTile / KSTEP;             // K chunks per lane
@@ -1485,26 +1488,36 @@ struct VerifyIo {
         uint32_t tk[KL], tv[VL], pk[KL], pv[VL];
 #pragma unroll
         for (int i = 0; i < KL; ++i) tk[i] = min(key0 + k0 + i * KSTEP, last_tok);
+        if constexpr (!kRowV) {
 #pragma unroll
-        for (int i = 0; i < VL; ++i) tv[i] = min(key0 + 4 * (k0 + i * KSTEP), last_tok);
+            for (int i = 0; i < VL; ++i) tv[i] = min(key0 + 4 * (k0 + i * KSTEP), last_tok);
+        }
         // every page id is requested before any is used: one LDS round trip
-        // per tile instead of one per load
+        // per tile instead of one per load (row-major V shares K's rows)
 #pragma unroll
         for (int i = 0; i < KL; ++i) pk[i] = (uint32_t)pids[(tk[i] >> lpt) - first];
+        if constexpr (!kRowV) {
 #pragma unroll
-        for (int i = 0; i < VL; ++i) pv[i] = (uint32_t)pids[(tv[i] >> lpt) - first];
+            for (int i = 0; i < VL; ++i) pv[i] = (uint32_t)pids[(tv[i] >> lpt) - first];
+        }
         __builtin_amdgcn_sched_barrier(0);
         // every tile is read by one workgroup once: nontemporal loads
         // (streaming reads measured ~8 % faster than ordinary loads)
 #pragma unroll
         for (int i = 0; i < KL; ++i) kr[i] = __builtin_nontemporal_load(row_ptr(k_head, pk[i], tk[i], ch));
+        if constexpr (kRowV) {
+            static_assert(4 * VL == KL, "V rows in the K slots' registers");
 #pragma unroll
-        for (int i = 0; i < VL; ++i)
+            for (int i = 0; i < KL; ++i) vr[i] = __builtin_nontemporal_load(row_ptr(v_head, pk[i], tk[i], ch));
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t tok = min(key0 + 4 * (k0 + i * KSTEP) + j, last_tok);
-                vr[4 * i + j] = __builtin_nontemporal_load(row_ptr(v_head, pv[i], tok, ch));
-            }
+            for (int i = 0; i < VL; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t tok = min(key0 + 4 * (k0 + i * KSTEP) + j, last_tok);
+                    vr[4 * i + j] = __builtin_nontemporal_load(row_ptr(v_head, pv[i], tok, ch));
+                }
+        }
     }
     // Keys past the sequence's last were loaded as copies of its last row
     // (load clamps them), so their V rows are finite and need no zeroing: the
@@ -1520,6 +1533,17 @@ struct VerifyIo {
 #pragma unroll
             for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(kr[i][j]), bf16hi(kr[i][j]));
             *(u32x4 *)(kt + key * (D * 2) + ((ch ^ k_swz<D>(key)) * 16)) = f;
+        }
+        if constexpr (kRowV) {
+#pragma unroll
+            for (int i = 0; i < KL; ++i) {
+                const uint32_t key = k0 + i * KSTEP;  // key & 3 == k0 & 3
+                u32x4 f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(vr[i][j]), bf16hi(vr[i][j]));
+                *(u32x4 *)(vt + key * (D * 2) + ((ch ^ v_swz(k0)) * 16)) = f;
+            }
+            return;
         }
 #pragma unroll
         for (int i = 0; i < VL; ++i) {
@@ -1664,6 +1688,8 @@ attn_verify_kernel(const VerifyParams vp) {
     f32x16 oacc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+    uint32_t voff[NT];
+    if constexpr (VerifyIo<D>::kRowV) pv_rows_offsets<D>(lane, voff);
     float m_run = -INFINITY;
     float l_run = 0.0f;
     for (uint32_t k = 0; k < k_pad; ++k) {
@@ -1689,7 +1715,8 @@ attn_verify_kernel(const VerifyParams vp) {
         }
         f16x8 pop[4];
         softmax_tile<D>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
-        pv_tile<D>(vt, pop, h, col, oacc);
+        if constexpr (VerifyIo<D>::kRowV) pv_tile_rows<D>(vt, voff, pop, oacc);
+        else pv_tile<D>(vt, pop, h, col, oacc);
     }
     const float l = xhalf_sum(l_run);
     if (32u * cw + col >= nvec) return;
