@@ -268,6 +268,18 @@ typedef struct safetyraise_kernel_gdn_args {
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
     safetyraise_kernel_context *context, const safetyraise_kernel_gdn_args *args);
 
+/* ABI v1 linear (safetyraise_kernel_linear, reference header :115-123) with
+ * device pointers: input [rows][cols] and output [rows][out_cols] f32 in
+ * device memory, queued on the context's stream and not waited for.  The
+ * same shape checks as linear (status 1); the input is not scanned for
+ * non-finite values (linear does that on the host, native/cpu/
+ * safetyraise_cpu.c:221-226): non-finite inputs give non-finite outputs.
+ * The weight is any handle from create_weight (dtype F32, F16 or BF16). */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear_device(
+    safetyraise_kernel_context *context, safetyraise_kernel_weight *weight, const float *input,
+    uint64_t input_rows, uint64_t input_cols, float *output, uint64_t output_rows,
+    uint64_t output_cols);
+
 #ifdef __cplusplus
 }
 #endif

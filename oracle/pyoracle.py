@@ -75,6 +75,8 @@ def lib() -> C.CDLL:
         L.sro_attention_rows.restype = i
         L.sro_attention_rows.argtypes = [_f32p, _f32p, _f32p, sz, _i64p, sz, sz, sz, i, opt_f32,
                                          opt_f32, f, f, sz, vp, i, vp, _f32p, i]
+        L.sro_linear.restype = i
+        L.sro_linear.argtypes = [_f32p, sz, sz, vp, C.c_uint32, sz, _f32p]
         L.sro_gdn_rows.restype = i
         L.sro_gdn_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, _f32p, _f32p, _f32p, sz, _f32p,
                                    f, sz, sz, sz, sz, _f32p, _f32p, _f32p]
@@ -244,4 +246,18 @@ def gdn_rows(qkv, z, a, b, a_log, dt_bias, conv_weight, kernel: int, norm, eps: 
                            f32(a_log), f32(dt_bias), f32(conv_weight).ravel(), kernel, f32(norm),
                            eps, key_heads, value_heads, key_dim, value_dim,
                            history.reshape(-1), state.reshape(-1), out.ravel()), "gdn_rows")
+    return out
+
+
+def linear(x, weight_bits: np.ndarray, dtype: int) -> np.ndarray:
+    """ABI v1 linear (native/cpu/safetyraise_cpu.c:203-239): x [rows, cols]
+    f32 times weight [out, cols]^T.  weight_bits holds the raw weight: float32
+    for dtype 1, uint16 bit patterns for dtype 2 (f16) and 3 (bf16)."""
+    x = f32(np.atleast_2d(x))
+    w = np.ascontiguousarray(weight_bits)
+    assert w.ndim == 2 and w.shape[1] == x.shape[1]
+    assert w.dtype == (np.float32 if dtype == 1 else np.uint16)
+    out = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    _ok(lib().sro_linear(x, x.shape[0], x.shape[1], w.ctypes.data, dtype, w.shape[0], out),
+        "linear")
     return out

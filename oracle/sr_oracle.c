@@ -532,3 +532,69 @@ done:
     free(recurrent);
     return status;
 }
+
+/* ---- ABI v1 linear (native/cpu/safetyraise_cpu.c:47-89, :203-239) ---- */
+
+/* IEEE binary16 -> binary32, exact for every input (normal, subnormal,
+ * zero, infinity and NaN payloads). */
+static float sro_half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t exponent = (h >> 10) & 0x1fu;
+    uint32_t fraction = h & 0x3ffu;
+    uint32_t bits;
+    if (exponent == 0u) {
+        if (fraction == 0u) {
+            bits = sign;
+        } else {
+            int e = -14;
+            while ((fraction & 0x400u) == 0u) {
+                fraction <<= 1;
+                --e;
+            }
+            bits = sign | ((uint32_t)(e + 127) << 23) | ((fraction & 0x3ffu) << 13);
+        }
+    } else if (exponent == 0x1fu) {
+        bits = sign | 0x7f800000u | (fraction << 13);
+    } else {
+        bits = sign | ((exponent + 112u) << 23) | (fraction << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+static float sro_weight_value(const void *weight, uint32_t dtype, size_t index) {
+    if (dtype == 1u) {
+        return ((const float *)weight)[index];
+    }
+    const uint16_t bits = ((const uint16_t *)weight)[index];
+    if (dtype == 2u) {
+        return sro_half_to_float(bits);
+    }
+    const uint32_t wide = (uint32_t)bits << 16;
+    float f;
+    memcpy(&f, &wide, sizeof f);
+    return f;
+}
+
+int sro_linear(const float *input, size_t rows, size_t cols, const void *weight,
+               uint32_t dtype, size_t out_features, float *output) {
+    if (dtype < 1u || dtype > 3u) {
+        return 1;
+    }
+    for (size_t i = 0; i < rows * cols; ++i) {
+        if (!isfinite(input[i])) {
+            return 1;
+        }
+    }
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t o = 0; o < out_features; ++o) {
+            float sum = 0.0f;
+            for (size_t c = 0; c < cols; ++c) {
+                sum += input[r * cols + c] * sro_weight_value(weight, dtype, o * cols + c);
+            }
+            output[r * out_features + o] = sum;
+        }
+    }
+    return 0;
+}

@@ -92,6 +92,13 @@ int sro_gdn_rows(const float *qkv, const float *z, const float *a, const float *
                  size_t key_heads, size_t value_heads, size_t key_dim, size_t value_dim,
                  float *history, float *state, float *out);
 
+/* ABI v1 linear (native/cpu/safetyraise_cpu.c:203-239): output[r][o] =
+ * sum over c, in order, of input[r][c] * weight[o][c] in f32, with the weight
+ * widened exactly from its dtype (1 = f32, 2 = f16 as :47-78, 3 = bf16 by
+ * shift).  Returns 1 for a non-finite input (:221-226) or an unknown dtype. */
+int sro_linear(const float *input, size_t rows, size_t cols, const void *weight,
+               uint32_t dtype, size_t out_features, float *output);
+
 #ifdef __cplusplus
 }
 #endif

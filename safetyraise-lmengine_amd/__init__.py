@@ -12,6 +12,9 @@ from .plugin import (  # noqa: F401
     CAP_DEVICE_STATE,
     CAP_GDN,
     DEVICE_POINTERS,
+    DTYPE_BF16,
+    DTYPE_F16,
+    DTYPE_F32,
     EXTENSION_SYMBOLS,
     GATED,
     INPUT_BF16,
@@ -23,6 +26,7 @@ from .plugin import (  # noqa: F401
     KvCache,
     NativeBackend,
     PluginError,
+    Weight,
     attention_forward,
     gdn_forward,
     library_path,

@@ -1,10 +1,11 @@
 // Context lifetime, the nine ABI v1 symbols and the shared host helpers.
 //
-// ABI v1 is declared in include/safetyraise_kernel.h.  This plugin reports
-// dtype_mask = 0, so the engine's loader never routes a projection here
-// (src/backend/mod.rs:259-264 falls back to its CPU matmul); linear and
-// create_weight exist because the loader requires every v1 symbol
-// (src/backend/mod.rs:553-575), and answer UNSUPPORTED_DTYPE.
+// ABI v1 is declared in include/safetyraise_kernel.h.  linear takes F32, F16
+// and BF16 weights (dtype_mask bits 1-3), kept on the device from
+// create_weight to destroy_weight, and runs on f32 MFMA (linear_kernels.hip);
+// the engine's loader routes a projection here when its weight format's bit
+// is set (src/backend/mod.rs:259-264) and falls back to its CPU matmul
+// otherwise.
 
 #include <cmath>
 #include <cstdio>
@@ -178,7 +179,8 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_context(
     if (hipStreamSynchronize(context->stream) != hipSuccess) {
         status = kDeviceError;
     }
-    for (DeviceBuffer *b : {&context->staging, &context->partials, &context->rope_scratch}) {
+    for (DeviceBuffer *b : {&context->staging, &context->partials, &context->rope_scratch,
+                            &context->linear_in, &context->linear_out}) {
         if (b->ptr != nullptr) (void)hipFree(b->ptr);
     }
     if (context->d_error_word != nullptr) (void)hipFree(context->d_error_word);
@@ -195,7 +197,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_get_capabilities(
     }
     out_capabilities->abi_version = SAFETYRAISE_KERNEL_ABI_VERSION;
     out_capabilities->struct_size = sizeof(safetyraise_kernel_capabilities);
-    out_capabilities->dtype_mask = 0;  // no linear weights: the engine keeps projections
+    out_capabilities->dtype_mask = (UINT64_C(1) << SAFETYRAISE_KERNEL_DTYPE_F32) |
+                                   (UINT64_C(1) << SAFETYRAISE_KERNEL_DTYPE_F16) |
+                                   (UINT64_C(1) << SAFETYRAISE_KERNEL_DTYPE_BF16);
     out_capabilities->device_kind = SAFETYRAISE_KERNEL_DEVICE_OTHER;
     out_capabilities->flags = SAFETYRAISE_MI355X_CAP_ATTENTION | SAFETYRAISE_MI355X_CAP_GDN |
                               SAFETYRAISE_MI355X_CAP_DEVICE_STATE;
@@ -207,17 +211,45 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_get_capabilities(
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_create_weight(
     safetyraise_kernel_context *context, const uint8_t *data, uint64_t byte_len, uint64_t rows,
     uint64_t cols, uint32_t dtype, safetyraise_kernel_weight **out_weight) {
-    (void)data;
-    (void)byte_len;
-    (void)rows;
-    (void)cols;
+    // native/cpu/safetyraise_cpu.c:140-189: byte_len must equal
+    // rows * cols * element size, and the bytes are copied before returning
     if (context == nullptr || out_weight == nullptr) {
         return fail(context, kInvalid, "weight arguments are invalid");
     }
-    char message[128];
-    snprintf(message, sizeof message,
-             "dtype %u is not supported: this plugin provides attention and GDN only", dtype);
-    return fail(context, kUnsupportedDtype, message);
+    if (dtype != SAFETYRAISE_KERNEL_DTYPE_F32 && dtype != SAFETYRAISE_KERNEL_DTYPE_F16 &&
+        dtype != SAFETYRAISE_KERNEL_DTYPE_BF16) {
+        char message[128];
+        snprintf(message, sizeof message, "weight dtype %u is not supported (F32, F16, BF16 are)",
+                 dtype);
+        return fail(context, kUnsupportedDtype, message);
+    }
+    const uint64_t element = dtype == SAFETYRAISE_KERNEL_DTYPE_F32 ? 4 : 2;
+    uint64_t count = 0, bytes = 0;
+    if (!checked_mul(rows, cols, &count) || !checked_mul(count, element, &bytes) ||
+        bytes != byte_len || (byte_len != 0 && data == nullptr)) {
+        return fail(context, kInvalid, "weight byte length does not match its shape and dtype");
+    }
+    if (rows > UINT32_MAX || cols > UINT32_MAX) {
+        return fail(context, kOverflow, "weight dimensions exceed 2^32 - 1");
+    }
+    auto *weight = new (std::nothrow) safetyraise_kernel_weight;
+    if (weight == nullptr) {
+        return fail(context, kNoMemory, "cannot allocate a weight handle");
+    }
+    weight->rows = rows;
+    weight->cols = cols;
+    weight->dtype = dtype;
+    if (bytes != 0) {
+        hipError_t e = hipMalloc(&weight->d_data, bytes);
+        if (e == hipSuccess) e = hipMemcpy(weight->d_data, data, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            if (weight->d_data != nullptr) (void)hipFree(weight->d_data);
+            delete weight;
+            return hip_fail(context, e, "create_weight");
+        }
+    }
+    *out_weight = weight;
+    return kOk;
 }
 
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_weight(
@@ -225,24 +257,89 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_weight(
     if (weight == nullptr) {
         return fail(context, kInvalid, "weight handle is NULL");
     }
+    int32_t status = kOk;
+    if (weight->d_data != nullptr) {
+        // queued linear calls may still read it
+        if (context != nullptr) SR_HIP(context, hipStreamSynchronize(context->stream));
+        const hipError_t e = hipFree(weight->d_data);
+        if (e != hipSuccess) status = hip_fail(context, e, "destroy_weight");
+    }
     delete weight;
+    return status;
+}
+
+namespace sr {
+// The shape rules of native/cpu/safetyraise_cpu.c:214-220.
+static int32_t check_linear(Ctx *ctx, const safetyraise_kernel_weight *w, const float *input,
+                            uint64_t in_rows, uint64_t in_cols, const float *output,
+                            uint64_t out_rows, uint64_t out_cols, uint64_t *in_count,
+                            uint64_t *out_count) {
+    if (w == nullptr || in_rows != out_rows || in_cols != w->cols || out_cols != w->rows ||
+        !checked_mul(in_rows, in_cols, in_count) || !checked_mul(out_rows, out_cols, out_count) ||
+        (*in_count != 0 && input == nullptr) || (*out_count != 0 && output == nullptr)) {
+        return fail(ctx, kInvalid, "linear shapes or pointers are invalid");
+    }
+    if (in_rows > UINT32_MAX || *in_count > (UINT64_MAX >> 3) || *out_count > (UINT64_MAX >> 3)) {
+        return fail(ctx, kOverflow, "linear dimensions are too large");
+    }
     return kOk;
 }
+}  // namespace sr
 
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear(
     safetyraise_kernel_context *context, safetyraise_kernel_weight *weight, const float *input,
     uint64_t input_rows, uint64_t input_cols, float *output, uint64_t output_rows,
     uint64_t output_cols) {
-    (void)input;
-    (void)input_rows;
-    (void)input_cols;
-    (void)output;
-    (void)output_rows;
-    (void)output_cols;
-    if (context == nullptr || weight == nullptr) {
-        return fail(context, kInvalid, "linear arguments are invalid");
+    if (context == nullptr) {
+        return kInvalid;
     }
-    return fail(context, kUnsupportedDtype, "linear is not provided by this plugin");
+    uint64_t in_count = 0, out_count = 0;
+    const int32_t st = check_linear(context, weight, input, input_rows, input_cols, output,
+                                    output_rows, output_cols, &in_count, &out_count);
+    if (st != kOk) return st;
+    // native/cpu/safetyraise_cpu.c:221-226: every input must be finite
+    for (uint64_t i = 0; i < in_count; ++i) {
+        if (!std::isfinite(input[i])) {
+            return fail(context, kInvalid, "linear input contains non-finite values");
+        }
+    }
+    if (out_count == 0) return kOk;
+    int32_t e = ensure_buffer(context, context->linear_in, (size_t)(in_count ? in_count : 1) * 4,
+                              false);
+    if (e != kOk) return e;
+    e = ensure_buffer(context, context->linear_out, (size_t)out_count * 4, false);
+    if (e != kOk) return e;
+    float *d_in = (float *)context->linear_in.ptr;
+    float *d_out = (float *)context->linear_out.ptr;
+    if (in_count != 0) {
+        SR_HIP(context, hipMemcpyAsync(d_in, input, in_count * 4, hipMemcpyHostToDevice,
+                                       context->stream));
+    }
+    SR_HIP(context, launch_linear(context->stream, d_in, weight->d_data, weight->dtype, d_out,
+                                  (uint32_t)input_rows, (uint32_t)weight->rows,
+                                  (uint32_t)weight->cols));
+    SR_HIP(context, hipMemcpyAsync(output, d_out, out_count * 4, hipMemcpyDeviceToHost,
+                                   context->stream));
+    SR_HIP(context, hipStreamSynchronize(context->stream));
+    return kOk;
+}
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear_device(
+    safetyraise_kernel_context *context, safetyraise_kernel_weight *weight, const float *input,
+    uint64_t input_rows, uint64_t input_cols, float *output, uint64_t output_rows,
+    uint64_t output_cols) {
+    if (context == nullptr) {
+        return kInvalid;
+    }
+    uint64_t in_count = 0, out_count = 0;
+    const int32_t st = check_linear(context, weight, input, input_rows, input_cols, output,
+                                    output_rows, output_cols, &in_count, &out_count);
+    if (st != kOk) return st;
+    if (out_count == 0) return kOk;
+    SR_HIP(context, launch_linear(context->stream, input, weight->d_data, weight->dtype, output,
+                                  (uint32_t)input_rows, (uint32_t)weight->rows,
+                                  (uint32_t)weight->cols));
+    return kOk;
 }
 
 SAFETYRAISE_KERNEL_EXPORT const char *safetyraise_kernel_last_error(

@@ -70,15 +70,20 @@ struct safetyraise_kernel_context {
     sr::DeviceBuffer staging;          // host-pointer mode device copies
     sr::DeviceBuffer partials;         // split-K partial (m, l, o) records
     sr::DeviceBuffer rope_scratch;     // prefill: per-row RoPE cos/sin
+    sr::DeviceBuffer linear_in;        // linear: the host input's device copy
+    sr::DeviceBuffer linear_out;       // linear: the output before it goes back
     float rope_theta = 0.0f;
     uint32_t rope_dim = 0;
     sr::RopeTable rope{};
 };
 
+// A linear weight [rows][cols] in its own dtype (F32, F16 or BF16), on the
+// device for the life of the handle.
 struct safetyraise_kernel_weight {
     uint64_t rows = 0;
     uint64_t cols = 0;
     uint32_t dtype = 0;
+    void *d_data = nullptr;
 };
 
 struct safetyraise_kernel_kv_pool {
@@ -231,6 +236,11 @@ struct GdnLaunch {
 };
 
 // Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
+// y[M][N] = x[M][K] . W[N][K]^T on f32 MFMA, W of dtype F32/F16/BF16
+// (linear_kernels.hip).
+hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
+                         float *y, uint32_t M, uint32_t N, uint32_t K);
+
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,
                       const uint32_t *rows, const uint32_t *row0, const uint32_t *parity, int nseq,
                       uint32_t total_rows);

@@ -88,6 +88,7 @@ EXTENSION_SYMBOLS = (
     "safetyraise_kernel_gdn_read",
     "safetyraise_kernel_gdn_write",
     "safetyraise_kernel_gdn_forward",
+    "safetyraise_kernel_linear_device",
 )
 
 
@@ -222,6 +223,7 @@ def _declare(lib: C.CDLL) -> None:
         "safetyraise_kernel_gdn_read": (i32, [vp, vp, u32, vp, vp]),
         "safetyraise_kernel_gdn_write": (i32, [vp, vp, u32, vp, vp]),
         "safetyraise_kernel_gdn_forward": (i32, [vp, C.POINTER(GdnArgs)]),
+        "safetyraise_kernel_linear_device": (i32, [vp, vp, vp, u64, u64, vp, u64, u64]),
     }
     for name, (res, args) in sig.items():
         if hasattr(lib, name):
@@ -340,24 +342,39 @@ class NativeBackend:
     def __exit__(self, *exc):
         self.close()
 
-    # -- v1 linear (the plugin reports no dtype; kept for ABI tests) ----------
-    def linear(self, weight: np.ndarray, inputs: np.ndarray) -> np.ndarray:
-        w = np.ascontiguousarray(weight, dtype=np.float32)
-        x = np.ascontiguousarray(inputs, dtype=np.float32)
-        rows, cols = x.shape
-        out_dim = w.shape[0]
+    # -- v1 linear (src/backend/mod.rs:259-333: prepare once, then call) -------
+    def create_weight(self, weight: np.ndarray, dtype: int = None) -> "Weight":
+        """A device copy of weight[out][cols]: float32 values (dtype F32), or
+        uint16 bit patterns with dtype F16 or BF16."""
+        w = np.ascontiguousarray(weight)
+        if dtype is None:
+            dtype = DTYPE_F32
+        if dtype == DTYPE_F32:
+            w = np.ascontiguousarray(w, dtype=np.float32)
+        elif w.dtype != np.uint16:
+            raise ValueError("F16/BF16 weights are passed as uint16 bit patterns")
         handle = C.c_void_p()
         self.check(self.lib.safetyraise_kernel_create_weight(
-            self.context, w.ctypes.data, w.nbytes, w.shape[0], w.shape[1], DTYPE_F32,
+            self.context, w.ctypes.data, w.nbytes, w.shape[0], w.shape[1], dtype,
             C.byref(handle)), "preparing a native weight")
+        return Weight(self, handle, w.shape[0], w.shape[1], dtype)
+
+    def linear(self, weight, inputs: np.ndarray, dtype: int = None) -> np.ndarray:
+        """inputs [rows][cols] times weight^T; weight is a Weight or an array
+        (prepared for this call only)."""
+        own = not isinstance(weight, Weight)
+        w = self.create_weight(weight, dtype) if own else weight
         try:
-            out = np.zeros((rows, out_dim), dtype=np.float32)
+            x = np.ascontiguousarray(inputs, dtype=np.float32)
+            rows, cols = x.shape
+            out = np.zeros((rows, w.rows), dtype=np.float32)
             self.check(self.lib.safetyraise_kernel_linear(
-                self.context, handle, x.ctypes.data, rows, cols, out.ctypes.data, rows, out_dim),
+                self.context, w.handle, x.ctypes.data, rows, cols, out.ctypes.data, rows, w.rows),
                 "native linear")
             return out
         finally:
-            self.lib.safetyraise_kernel_destroy_weight(self.context, handle)
+            if own:
+                w.destroy()
 
     # -- extension ---------------------------------------------------------
     def set_stream(self, stream_handle: Optional[int]) -> None:
@@ -366,6 +383,19 @@ class NativeBackend:
 
     def synchronize(self) -> None:
         self.check(self.lib.safetyraise_kernel_synchronize(self.context), "synchronizing")
+
+
+class Weight:
+    """A prepared native weight (create_weight / destroy_weight)."""
+
+    def __init__(self, backend: NativeBackend, handle, rows: int, cols: int, dtype: int):
+        self.backend, self.handle, self.rows, self.cols, self.dtype = backend, handle, rows, cols, dtype
+
+    def destroy(self) -> None:
+        if self.handle is not None:
+            self.backend.check(self.backend.lib.safetyraise_kernel_destroy_weight(
+                self.backend.context, self.handle), "destroying a native weight")
+            self.handle = None
 
 
 class KvCache:

@@ -1,0 +1,122 @@
+"""GPU parity of ABI v1 linear (native/cpu/safetyraise_cpu.c:140-239) through the C-ABI.
+
+linear computes output[r][o] = sum_c input[r][c] * weight[o][c] in f32 with
+the weight widened exactly from F32, F16 or BF16.  The plugin sums in another
+order (f32 MFMA over k blocks, four partial sums), so random inputs are held
+to |d| <= 1e-5 * sum_c |input * weight| + 1e-4 * |ref| (the error bound of a
+reordered f32 sum scales with the magnitude of the terms, not of the result),
+and integer-valued inputs, whose every partial sum is exact in f32, must match
+the oracle bit for bit.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as O
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16 = 1, 2, 3
+
+
+@pytest.fixture
+def rng(request):
+    return np.random.default_rng(abs(hash(request.node.name)) % (2 ** 32))
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+    return torch
+
+
+def weight_bits(w: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == F32:
+        return np.ascontiguousarray(w, np.float32)
+    if dtype == F16:
+        return np.ascontiguousarray(w.astype(np.float16).view(np.uint16))
+    return np.ascontiguousarray((O.bf16_round(w.astype(np.float32)).view(np.uint32) >> 16)
+                                .astype(np.uint16))
+
+
+def widened(bits: np.ndarray, dtype: int) -> np.ndarray:
+    if dtype == F32:
+        return bits.astype(np.float64)
+    if dtype == F16:
+        return bits.view(np.float16).astype(np.float64)
+    return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def test_known_answer_capabilities_and_errors(pkg, backend):
+    # src/backend/mod.rs:713-724
+    caps = backend.capabilities
+    assert caps.dtype_mask == (1 << F32) | (1 << F16) | (1 << BF16)
+    w = np.array([[1.0, 0.0, -1.0], [2.0, 3.0, 4.0]], np.float32)
+    x = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], np.float32)
+    expected = np.array([[-2.0, 20.0], [-2.0, 47.0]], np.float32)
+    prepared = backend.create_weight(w)
+    try:
+        assert np.array_equal(backend.linear(prepared, x), expected)
+        assert np.array_equal(backend.linear(prepared, x), expected)  # the weight is reusable
+        with pytest.raises(pkg.PluginError) as err:
+            backend.linear(prepared, np.array([[np.nan, 2.0, 3.0]], np.float32))
+        assert err.value.status == 1
+        with pytest.raises(pkg.PluginError) as err:  # input width != weight cols
+            backend.linear(prepared, np.ones((2, 4), np.float32))
+        assert err.value.status == 1
+    finally:
+        prepared.destroy()
+    lib, ctx = backend.lib, backend.context
+    h = C.c_void_p()
+    # byte length that does not match rows * cols * element size
+    assert lib.safetyraise_kernel_create_weight(ctx, w.ctypes.data, w.nbytes - 4, 2, 3, F32,
+                                                C.byref(h)) == 1
+    # a dtype outside the mask
+    assert lib.safetyraise_kernel_create_weight(ctx, w.ctypes.data, 6, 2, 3, 4, C.byref(h)) == 2
+    assert lib.safetyraise_kernel_destroy_weight(ctx, None) == 1
+
+
+@pytest.mark.parametrize("dtype", [F32, F16, BF16])
+@pytest.mark.parametrize("rows,cols,out", [(1, 4096, 512), (7, 96, 33), (64, 1001, 257),
+                                           (17, 3, 5), (40, 130, 16)])
+def test_random_inputs_match_the_oracle(backend, rng, dtype, rows, cols, out):
+    x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((out, cols)), dtype)
+    got = backend.linear(bits, x, dtype)
+    ref = O.linear(x, bits, dtype)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, dtype)).T
+    bad = np.abs(got - ref) > 1e-5 * mag + 1e-4 * np.abs(ref)
+    assert not bad.any(), (dtype, rows, cols, out, np.abs(got - ref).max())
+
+
+@pytest.mark.parametrize("dtype", [F32, F16, BF16])
+def test_integer_inputs_are_bit_exact(backend, rng, dtype):
+    # every product and partial sum is an integer below 2^24: exact in f32 in
+    # any order, so the plugin must equal the reference's sequential sum
+    x = rng.integers(-8, 9, size=(21, 515)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(70, 515)).astype(np.float32)
+    bits = weight_bits(w, dtype)
+    assert np.array_equal(backend.linear(bits, x, dtype), O.linear(x, bits, dtype))
+
+
+def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod):
+    torch = torch_mod
+    x = rng.standard_normal((9, 256)).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((130, 256)), BF16)
+    prepared = backend.create_weight(bits, BF16)
+    try:
+        host = backend.linear(prepared, x)
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.zeros((9, 130), device="cuda")
+        backend.check(backend.lib.safetyraise_kernel_linear_device(
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, 256,
+            C.c_void_p(dy.data_ptr()), 9, 130), "linear_device")
+        backend.synchronize()
+        assert np.array_equal(dy.cpu().numpy(), host)
+        # the same shape checks as linear
+        assert backend.lib.safetyraise_kernel_linear_device(
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, 255,
+            C.c_void_p(dy.data_ptr()), 9, 130) == 1
+    finally:
+        prepared.destroy()

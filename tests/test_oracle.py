@@ -7,6 +7,7 @@ brute force written here in numpy.  Tolerances are stated per test.
 import ctypes
 import ctypes.util
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -448,3 +449,50 @@ def test_gdn_rows_match_f64_brute_force(hk, hv, dk, dv, K):
         close(out[r], exp, 1e-5, 1e-5)
     close(state, s64, 1e-5, 1e-5)
     close(hist, h64, 0.0, 0.0)
+
+
+# ---------------------------------------------------------------------------
+# ABI v1 linear (native/cpu/safetyraise_cpu.c:203-239)
+# ---------------------------------------------------------------------------
+
+def test_linear_known_answer_and_non_finite_input():
+    # src/backend/mod.rs:713-724
+    w = np.array([[1.0, 0.0, -1.0], [2.0, 3.0, 4.0]], np.float32)
+    x = np.array([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], np.float32)
+    assert np.array_equal(O.linear(x, w, 1), np.array([[-2.0, 20.0], [-2.0, 47.0]], np.float32))
+    with pytest.raises(O.OracleError):
+        O.linear(np.array([[np.nan, 2.0, 3.0]], np.float32), w, 1)
+
+
+@pytest.mark.parametrize("dtype", [2, 3])
+def test_linear_widens_every_16_bit_pattern_exactly(dtype):
+    # one input of 1.0 against a weight column holding all 65536 patterns:
+    # f16 widening is exact (numpy's float16), bf16 widening is the shift
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(-1, 1)
+    got = O.linear(np.ones((1, 1), np.float32), bits, dtype)[0]
+    if dtype == 2:
+        want = bits.view(np.float16).astype(np.float32)[:, 0]
+    else:
+        want = (bits.astype(np.uint32) << 16).view(np.float32)[:, 0]
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])  # 0.0 + (-0.0) is +0.0; == treats them alike
+
+
+REF_PLUGIN = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "libsafetyraise_cpu.so"
+
+
+@pytest.mark.skipif(not REF_PLUGIN.exists(), reason="reference C plugin not built (oracle/_ref)")
+@pytest.mark.parametrize("rows,cols,out", [(1, 37, 5), (5, 96, 19), (3, 1, 4)])
+def test_linear_matches_the_reference_plugin_bit_for_bit(pkg, rows, cols, out):
+    # the reference's own C plugin (built from native/cpu/safetyraise_cpu.c)
+    # for the dtypes it supports: f32 and f16
+    backend = pkg.NativeBackend.load(REF_PLUGIN)
+    try:
+        x = (3 * RNG.standard_normal((rows, cols))).astype(np.float32)
+        w32 = RNG.standard_normal((out, cols)).astype(np.float32)
+        assert np.array_equal(backend.linear(w32, x), O.linear(x, w32, 1))
+        w16 = RNG.standard_normal((out, cols)).astype(np.float16).view(np.uint16)
+        assert np.array_equal(backend.linear(w16, x, pkg.DTYPE_F16), O.linear(x, w16, 2))
+    finally:
+        backend.close()
