@@ -43,7 +43,8 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "prefill", "verify", "gdn-decode", "gdn-prefill", "copy"])
+                   choices=["decode", "prefill", "verify", "gdn-decode", "gdn-prefill", "linear",
+                            "copy"])
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
     p.add_argument("--prefill-steps", type=int, default=5)
@@ -556,7 +557,7 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("gdn_decode_qwen35"),
-            "kernel": "gdn_delta_kernel + gdn_norm_gate_kernel",
+            "kernel": "gdn_head_kernel<512, ConvK<4>>",
             "launch_us_mean": round(float(call_us.mean()), 2),
             "bytes_per_launch": int(per_layer),
         },
@@ -715,6 +716,117 @@ def cpu_baseline_gdn(pool, ids_c, qkv_dev, layer, hk, hv, dk, dv, K, nseq, rows,
     return {"value": round(per_item * nseq / t / scale, 3), "unit": unit, "cores": 1,
             "kind": "port",
             "sample": f"{nseq} sequence(s) x {rows} row(s) of the same layer shape, f32 oracle",
+            "ms": round(t * 1e3, 2)}
+
+
+# Qwen3-8B decoder layer projections (out, in): q, k, v, o, gate, up, down
+LINEAR_SHAPES = ((4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096),
+                 (12288, 4096), (12288, 4096), (4096, 12288))
+
+
+def bench_linear(args, torch, pkg, steps, warmup, rows=16):
+    """ABI v1 linear (the next component after the attention / GDN rows): the
+    seven projections of one Qwen3-8B decoder layer (bf16 weights, 386 MB)
+    for a decode batch of 16 rows, through the device-pointer entry
+    (safetyraise_kernel_linear_device), inputs resident on the GPU.  One step =
+    the seven calls.  HBM-bound: algorithmic bytes = the weights plus the f32
+    inputs and outputs."""
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0006)
+    weights, xs, ys = [], [], []
+    for out_f, in_f in LINEAR_SHAPES:
+        w = (torch.randn((out_f, in_f), generator=gen, device="cuda") * 0.02).bfloat16()
+        bits = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        weights.append(backend.create_weight(bits, pkg.DTYPE_BF16))
+        xs.append(torch.randn((rows, in_f), generator=gen, device="cuda"))
+        ys.append(torch.empty((rows, out_f), device="cuda"))
+        del w, bits
+    fn = backend.lib.safetyraise_kernel_linear_device
+    ctx = backend.context
+
+    def run(events=None):
+        for i, (out_f, in_f) in enumerate(LINEAR_SHAPES):
+            if events is not None:
+                events[i][0].record(stream)
+            st = fn(ctx, weights[i].handle, C.c_void_p(xs[i].data_ptr()), rows, in_f,
+                    C.c_void_p(ys[i].data_ptr()), rows, out_f)
+            if events is not None:
+                events[i][1].record(stream)
+            if st != 0:
+                backend.check(st, "linear_device")
+
+    for _ in range(warmup):
+        run()
+    backend.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(steps):
+        run()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    backend.synchronize()
+    run()
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in LINEAR_SHAPES] for _ in range(steps)]
+    for s in range(steps):
+        run(ev[s])
+    torch.cuda.synchronize()
+    per_call = [o * i * 2 + rows * (i + o) * 4 for o, i in LINEAR_SHAPES]
+    per_step = sum(per_call)
+    ms = t0.elapsed_time(t1) / steps
+    value = per_step / (ms * 1e-3) / 1e9
+    # the dominant call shape for the roofline: gate/up (12288 x 4096)
+    big = [4, 5]
+    big_us = np.array([[ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e3 for i in big]
+                       for s in range(steps)])
+    achieved = per_call[4] / (big_us.mean() * 1e-6) / 1e9
+    result = {
+        "workload": f"Qwen3-8B decoder-layer projections (q/k/v/o/gate/up/down, bf16 weights, "
+                    f"386 MB), {rows} rows, f32 in/out, device pointers",
+        "value": round(value, 2), "unit": "GB/s",
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "dtype": "f32",
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles("linear_qwen3_8b"),
+            "kernel": "linear_kernel<BF16> (12288 x 4096 gate/up calls)",
+            "launch_us_mean": round(float(big_us.mean()), 2),
+            "bytes_per_launch": int(per_call[4]),
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_linear(weights[0], xs[0], rows)
+    for w in weights:
+        w.destroy()
+    backend.close()
+    return result
+
+
+def cpu_baseline_linear(weight, x_dev, rows):
+    """The oracle's linear (the reference CPU plugin's loop, 1 thread) on the q
+    projection (4096 x 4096 bf16) for 4 of the rows, as weight GB/s."""
+    from oracle import pyoracle as O
+
+    out_f, in_f = LINEAR_SHAPES[0]
+    rng = np.random.default_rng(11)
+    bits = (rng.integers(0, 1 << 16, size=(out_f, in_f), dtype=np.uint32) & 0x3fff).astype(np.uint16)
+    x = x_dev[:4].cpu().numpy()
+    t0 = time.perf_counter()
+    O.linear(x, bits, 3)
+    t = time.perf_counter() - t0
+    call_bytes = out_f * in_f * 2  # the weight stream the GPU figure counts, per call
+    return {"value": round(call_bytes / (t / 4 * rows) / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "q projection (4096 x 4096 bf16) for 4 rows, f32 oracle (the reference "
+                      "plugin's loop), scaled to the 16-row call",
             "ms": round(t * 1e3, 2)}
 
 
@@ -912,6 +1024,7 @@ def main():
             result["verify"] = bench_verify(args, torch, pkg, 5, 2)
             result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 10, 3)
             result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 3, 1)
+            result["linear"] = bench_linear(args, torch, pkg, 10, 3)
     elif args.workload == "verify":
         result = bench_verify(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "MTP verify attention GB/s", "n_gpus": 1, "higher_is_better": True,
@@ -923,6 +1036,11 @@ def main():
         result = {"metric": "GDN " + args.workload[4:] + " " + result["unit"], "n_gpus": 1,
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                   "data": "synthetic", "config": {"workload": result.pop("workload")}, **result}
+    elif args.workload == "linear":
+        result = bench_linear(args, torch, pkg, args.steps, args.warmup)
+        result = {"metric": "linear weight-stream GB/s", "n_gpus": 1, "higher_is_better": True,
+                  "scaling": "weak", "vs_baseline": None, "data": "synthetic",
+                  "config": {"workload": result.pop("workload")}, **result}
     elif args.workload == "prefill":
         result = bench_prefill(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "prefill attn TFLOP/s, Qwen3-8B GQA shape", "n_gpus": 1,

@@ -42,28 +42,34 @@ __device__ __forceinline__ float widen(const void *w, size_t i) {
     }
 }
 
-// Elements k .. k+3 of a row starting at element `row` (zeros past K).
-// kVec: K % 4 == 0, so a block start k < K has all four in range and the
-// row start is 16-byte aligned for f32 (8-byte for 16-bit weights).
+// Elements k .. k+3 of a row starting at element `row`, those from `lim` on
+// replaced by 0.  The reads themselves are clamped into the row (K >= 1;
+// kVec: K a multiple of 4), and the zeros are selected after the load: a
+// load behind a branch would make later waits wait for every load in flight.
+// kVec: the row start is 16-byte aligned for f32 (8-byte for 16-bit weights).
 template <int DT, bool kVec>
-__device__ __forceinline__ f32x4 load4(const void *base, size_t row, uint32_t k, uint32_t K) {
-    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+__device__ __forceinline__ f32x4 load4(const void *base, size_t row, uint32_t k, uint32_t K,
+                                       uint32_t lim) {
+    f32x4 v;
     if constexpr (kVec) {
-        if (k < K) {
-            if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F32) {
-                v = *(const f32x4 *)((const float *)base + row + k);
-            } else if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F16) {
-                v = __builtin_convertvector(*(const f16x4 *)((const _Float16 *)base + row + k), f32x4);
-            } else {
-                const uint2 u = *(const uint2 *)((const uint16_t *)base + row + k);
-                v = f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                          __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
-            }
+        const size_t i = row + min(k, K - 4);
+        if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F32) {
+            v = *(const f32x4 *)((const float *)base + i);
+        } else if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F16) {
+            v = __builtin_convertvector(*(const f16x4 *)((const _Float16 *)base + i), f32x4);
+        } else {
+            const uint2 u = *(const uint2 *)((const uint16_t *)base + i);
+            v = f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
         }
+        const bool live = k < lim;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = live ? v[j] : 0.0f;
     } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (k + j < K) v[j] = widen<DT>(base, row + k + j);
+            const float e = widen<DT>(base, row + min(k + j, K - 1));
+            v[j] = k + j < lim ? e : 0.0f;
         }
     }
     return v;
@@ -79,31 +85,78 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     const uint32_t r = lane & 15, g = lane >> 4;
     const uint32_t n0 = blockIdx.x * kLinTile, m0 = blockIdx.y * kLinTile;
     // rows past M / N read the last row and their results are not stored
+    if (K == 0) {  // empty sums (uniform): zeros
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = m0 + 4 * g + i, n = n0 + r;
+                if (m < M && n < N) y[(size_t)m * N + n] = 0.0f;
+            }
+        }
+        return;
+    }
     const size_t xrow = (size_t)min(m0 + r, M - 1) * K;
     const size_t wrow = (size_t)min(n0 + r, N - 1) * K;
     const uint32_t nblk = (K + 15) / 16;
     const uint32_t b0 = (uint32_t)((uint64_t)nblk * wave / kLinWaves);
     const uint32_t b1 = (uint32_t)((uint64_t)nblk * (wave + 1) / kLinWaves);
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t b = b0; b < b1; ++b) {
-        const uint32_t k = 16 * b + 4 * g;
-        const f32x4 a = load4<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K);
-        const f32x4 c = load4<DT, kVec>(w, wrow, k, K);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, c.x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, c.y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, c.z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, c.w, acc, 0, 0, 0);
+    // this wave's k range ends at kend: loads past it read zeros, so a group
+    // that runs past the range adds nothing (and no block is counted twice)
+    const uint32_t kend = min(16 * b1, K);
+    // groups of kGroup blocks in two register sets: while the MFMAs of one
+    // set run, the loads of the other are in flight (the sets alternate
+    // explicitly, so the compiler cannot merge them into one and wait for
+    // loads it has just issued)
+    constexpr int kGroup = 8;
+    f32x4 xa[kGroup], wa[kGroup], xb[kGroup], wb[kGroup];
+    auto load_group = [&](uint32_t b, f32x4 (&xv)[kGroup], f32x4 (&wv)[kGroup])
+                          __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            const uint32_t k = 16 * (b + j) + 4 * g;
+            xv[j] = load4<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K, kend);
+            wv[j] = load4<DT, kVec>(w, wrow, k, K, kend);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // four accumulation chains (block j of a group feeds chain j % 4), so
+    // consecutive MFMAs do not wait for each other's results
+    constexpr int kChains = 4;
+    f32x4 acc4[kChains];
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) acc4[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mfma_group = [&](const f32x4 (&xv)[kGroup], const f32x4 (&wv)[kGroup])
+                          __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            f32x4 &a = acc4[j % kChains];
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].x, wv[j].x, a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].y, wv[j].y, a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].z, wv[j].z, a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].w, wv[j].w, a, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // groups past the range load zeros (clamped reads) and add nothing
+    load_group(b0, xa, wa);
+    for (uint32_t b = b0; b < b1; b += 2 * kGroup) {
+        load_group(b + kGroup, xb, wb);
+        mfma_group(xa, wa);
+        load_group(b + 2 * kGroup, xa, wa);
+        mfma_group(xb, wb);
     }
+    const f32x4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
     if (wave > 0) red[wave - 1][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
+    f32x4 sum = acc;
 #pragma unroll
-    for (int j = 0; j < kLinWaves - 1; ++j) acc += red[j][lane];
+    for (int j = 0; j < kLinWaves - 1; ++j) sum += red[j][lane];
     const uint32_t n = n0 + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t m = m0 + 4 * g + i;
-        if (m < M && n < N) y[(size_t)m * N + n] = acc[i];
+        if (m < M && n < N) y[(size_t)m * N + n] = sum[i];
     }
 }
 
