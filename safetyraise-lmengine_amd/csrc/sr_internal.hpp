@@ -235,12 +235,12 @@ struct GdnLaunch {
     bool bf16_in;
 };
 
-// Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
 // y[M][N] = x[M][K] . W[N][K]^T on f32 MFMA, W of dtype F32/F16/BF16
 // (linear_kernels.hip).
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
                          float *y, uint32_t M, uint32_t N, uint32_t K);
 
+// Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,
                       const uint32_t *rows, const uint32_t *row0, const uint32_t *parity, int nseq,
                       uint32_t total_rows);
