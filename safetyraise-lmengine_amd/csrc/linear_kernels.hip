@@ -7,17 +7,23 @@
 // v_mfma_f32_16x16x4f32, so every product is an f32 product and only the
 // order of the sum differs from the reference (f32 tolerance, not bf16).
 //
-// Work split.  A workgroup owns 16 rows x 16 outputs; its four waves take
-// contiguous quarters of K and meet in LDS.  Decode-sized calls (M <= 16)
-// thus launch N/16 workgroups that each stream their 16 weight rows once,
-// which is the HBM-bound regime the ABI's projections live in; each k-step
-// loads 16 bytes of x and 4 weight elements per lane and feeds 4 MFMAs.
+// Work split.  A workgroup owns 16 rows x 16 outputs and a contiguous range
+// of K; its four waves take quarters of that range and meet in LDS.
+// Decode-sized calls (M <= 16) thus stream every weight row once, which is
+// the HBM-bound regime the ABI's projections live in; each k-step loads 16
+// bytes of x and 4 weight elements per lane and feeds 4 MFMAs.  A call with
+// fewer tiles than kLinWgPerCu workgroups per CU splits K over up to
+// kLinMaxSplits workgroups per tile (grid z): those write partial sums and
+// a second kernel adds them in split order, so results do not depend on
+// timing.
 //
 // Operand order.  For MFMA t of a 16-wide k block, lane (r = lane % 16,
 // g = lane / 16) feeds A = x[row r][k0 + 4g + t] and B = W[output r][same k]:
 // the four MFMAs cover the block's 16 k values with each lane reading 4
 // consecutive ones (any order of k gives the same sum; A and B share it).
 // The accumulator then holds y[row 4g + i][output r] in element i.
+
+#include <algorithm>
 
 #include "sr_internal.hpp"
 #include "sr_device.hpp"
@@ -30,6 +36,9 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLinTile = 16;   // rows and outputs per workgroup
 constexpr int kLinWaves = 4;   // waves splitting K
+constexpr uint32_t kLinWgPerCu = 1;    // workgroups per CU a call aims for
+constexpr uint32_t kLinMaxSplits = 8;  // K splits per tile at most
+constexpr uint32_t kLinMinSplitK = 512;  // K per split at least (8 blocks per wave)
 
 template <int DT>
 __device__ __forceinline__ float widen(const void *w, size_t i) {
@@ -75,6 +84,7 @@ __device__ __forceinline__ f32x4 load4(const void *base, size_t row, uint32_t k,
     return v;
 }
 
+// y: the output, or (grid z > 1) partial sums [grid z][M][N]
 template <int DT, bool kVec>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, const void *w,
                                                                  float *y, uint32_t M, uint32_t N,
@@ -97,9 +107,12 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     }
     const size_t xrow = (size_t)min(m0 + r, M - 1) * K;
     const size_t wrow = (size_t)min(n0 + r, N - 1) * K;
+    y += (size_t)blockIdx.z * M * N;
     const uint32_t nblk = (K + 15) / 16;
-    const uint32_t b0 = (uint32_t)((uint64_t)nblk * wave / kLinWaves);
-    const uint32_t b1 = (uint32_t)((uint64_t)nblk * (wave + 1) / kLinWaves);
+    const uint32_t s0 = (uint32_t)((uint64_t)nblk * blockIdx.z / gridDim.z);
+    const uint32_t s1 = (uint32_t)((uint64_t)nblk * (blockIdx.z + 1) / gridDim.z);
+    const uint32_t b0 = s0 + (uint32_t)((uint64_t)(s1 - s0) * wave / kLinWaves);
+    const uint32_t b1 = s0 + (uint32_t)((uint64_t)(s1 - s0) * (wave + 1) / kLinWaves);
     // this wave's k range ends at kend: loads past it read zeros, so a group
     // that runs past the range adds nothing (and no block is counted twice)
     const uint32_t kend = min(16 * b1, K);
@@ -160,10 +173,25 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     }
 }
 
+// y[i] = sum over z < splits of part[z][i], added in z order (splits <=
+// kLinMaxSplits; all loads are issued before the first add)
+__global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part, float *y,
+                                                               uint32_t count, uint32_t splits) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= count) return;
+    float v[kLinMaxSplits];
+#pragma unroll
+    for (uint32_t z = 0; z < kLinMaxSplits; ++z) v[z] = part[(size_t)min(z, splits - 1) * count + i];
+    float s = v[0];
+#pragma unroll
+    for (uint32_t z = 1; z < kLinMaxSplits; ++z) s = z < splits ? s + v[z] : s;
+    y[i] = s;
+}
+
 template <int DT>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
-               uint32_t K) {
-    const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile);
+               uint32_t K, uint32_t splits) {
+    const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile, splits);
     if ((K & 3u) == 0) {
         hipLaunchKernelGGL((linear_kernel<DT, true>), grid, dim3(64 * kLinWaves), 0, stream, x, w, y,
                            M, N, K);
@@ -175,22 +203,47 @@ void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint
 
 }  // namespace
 
+uint32_t linear_splits(uint32_t M, uint32_t N, uint32_t K, int num_cus) {
+    const uint64_t tiles = (uint64_t)((N + kLinTile - 1) / kLinTile) * ((M + kLinTile - 1) / kLinTile);
+    const uint64_t target = (uint64_t)kLinWgPerCu * (uint64_t)(num_cus > 0 ? num_cus : 1);
+    if (tiles == 0 || tiles >= target) return 1;
+    uint64_t s = (target + tiles - 1) / tiles;
+    s = std::min<uint64_t>(s, K / kLinMinSplitK);
+    s = std::min<uint64_t>(s, kLinMaxSplits);
+    return s < 1 ? 1u : (uint32_t)s;
+}
+
+size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, int num_cus) {
+    const uint32_t s = linear_splits(M, N, K, num_cus);
+    return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
+}
+
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
-                         float *y, uint32_t M, uint32_t N, uint32_t K) {
+                         float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
+                         int num_cus) {
     if (M == 0 || N == 0) return hipSuccess;
     if (M > 65535u * kLinTile) return hipErrorInvalidValue;  // grid y limit
+    const uint32_t splits = linear_splits(M, N, K, num_cus);
+    if (splits > 1 && scratch == nullptr) return hipErrorInvalidValue;
+    float *dst = splits > 1 ? scratch : y;
     switch (dtype) {
         case SAFETYRAISE_KERNEL_DTYPE_F32:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, y, M, N, K);
+            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, dst, M, N, K, splits);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_F16:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, y, M, N, K);
+            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, dst, M, N, K, splits);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_BF16:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, y, M, N, K);
+            launch_dt<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, dst, M, N, K, splits);
             break;
         default:
             return hipErrorInvalidValue;
+    }
+    if (splits > 1) {
+        // splits > 1 only when tiles < kLinWgPerCu * CUs, so M * N is small
+        const uint32_t count = M * N;
+        hipLaunchKernelGGL(linear_split_sum_kernel, dim3((count + 255) / 256), dim3(256), 0, stream,
+                           scratch, y, count, splits);
     }
     return hipGetLastError();
 }

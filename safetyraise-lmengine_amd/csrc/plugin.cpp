@@ -180,7 +180,8 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_context(
         status = kDeviceError;
     }
     for (DeviceBuffer *b : {&context->staging, &context->partials, &context->rope_scratch,
-                            &context->linear_in, &context->linear_out}) {
+                            &context->linear_in, &context->linear_out,
+                            &context->linear_part}) {
         if (b->ptr != nullptr) (void)hipFree(b->ptr);
     }
     if (context->d_error_word != nullptr) (void)hipFree(context->d_error_word);
@@ -284,6 +285,19 @@ static int32_t check_linear(Ctx *ctx, const safetyraise_kernel_weight *w, const 
     }
     return kOk;
 }
+
+// The partial-sum buffer of a call that splits K (nullptr when it does not).
+static int32_t linear_scratch(Ctx *ctx, const safetyraise_kernel_weight *w, uint64_t rows,
+                              float **part) {
+    const size_t bytes = linear_scratch_bytes((uint32_t)rows, (uint32_t)w->rows,
+                                              (uint32_t)w->cols, ctx->num_cus);
+    *part = nullptr;
+    if (bytes == 0) return kOk;
+    const int32_t e = ensure_buffer(ctx, ctx->linear_part, bytes, false);
+    if (e != kOk) return e;
+    *part = (float *)ctx->linear_part.ptr;
+    return kOk;
+}
 }  // namespace sr
 
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear(
@@ -309,6 +323,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear(
     if (e != kOk) return e;
     e = ensure_buffer(context, context->linear_out, (size_t)out_count * 4, false);
     if (e != kOk) return e;
+    float *part = nullptr;
+    e = linear_scratch(context, weight, input_rows, &part);
+    if (e != kOk) return e;
     float *d_in = (float *)context->linear_in.ptr;
     float *d_out = (float *)context->linear_out.ptr;
     if (in_count != 0) {
@@ -317,7 +334,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear(
     }
     SR_HIP(context, launch_linear(context->stream, d_in, weight->d_data, weight->dtype, d_out,
                                   (uint32_t)input_rows, (uint32_t)weight->rows,
-                                  (uint32_t)weight->cols));
+                                  (uint32_t)weight->cols, part, context->num_cus));
     SR_HIP(context, hipMemcpyAsync(output, d_out, out_count * 4, hipMemcpyDeviceToHost,
                                    context->stream));
     SR_HIP(context, hipStreamSynchronize(context->stream));
@@ -336,9 +353,12 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear_device(
                                     output_rows, output_cols, &in_count, &out_count);
     if (st != kOk) return st;
     if (out_count == 0) return kOk;
+    float *part = nullptr;
+    const int32_t e = linear_scratch(context, weight, input_rows, &part);
+    if (e != kOk) return e;
     SR_HIP(context, launch_linear(context->stream, input, weight->d_data, weight->dtype, output,
                                   (uint32_t)input_rows, (uint32_t)weight->rows,
-                                  (uint32_t)weight->cols));
+                                  (uint32_t)weight->cols, part, context->num_cus));
     return kOk;
 }
 

@@ -72,6 +72,7 @@ struct safetyraise_kernel_context {
     sr::DeviceBuffer rope_scratch;     // prefill: per-row RoPE cos/sin
     sr::DeviceBuffer linear_in;        // linear: the host input's device copy
     sr::DeviceBuffer linear_out;       // linear: the output before it goes back
+    sr::DeviceBuffer linear_part;      // linear: partial sums of calls that split K
     float rope_theta = 0.0f;
     uint32_t rope_dim = 0;
     sr::RopeTable rope{};
@@ -236,9 +237,12 @@ struct GdnLaunch {
 };
 
 // y[M][N] = x[M][K] . W[N][K]^T on f32 MFMA, W of dtype F32/F16/BF16
-// (linear_kernels.hip).
+// (linear_kernels.hip).  scratch holds linear_scratch_bytes(...) bytes of
+// partial sums (none when that is 0) for calls that split K.
+size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, int num_cus);
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
-                         float *y, uint32_t M, uint32_t N, uint32_t K);
+                         float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
+                         int num_cus);
 
 // Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,

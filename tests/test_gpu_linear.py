@@ -6,7 +6,9 @@ order (f32 MFMA over k blocks, four partial sums), so random inputs are held
 to |d| <= 1e-5 * sum_c |input * weight| + 1e-4 * |ref| (the error bound of a
 reordered f32 sum scales with the magnitude of the terms, not of the result),
 and integer-valued inputs, whose every partial sum is exact in f32, must match
-the oracle bit for bit.
+the oracle bit for bit.  Calls with few output tiles split K over several
+workgroups whose partial sums a second kernel adds (shapes (1, 4096, 512),
+(3, 2001, 100), (5, 1030, 20) and the 3072-column device call do).
 """
 import ctypes as C
 
@@ -79,7 +81,8 @@ def test_known_answer_capabilities_and_errors(pkg, backend):
 
 @pytest.mark.parametrize("dtype", [F32, F16, BF16])
 @pytest.mark.parametrize("rows,cols,out", [(1, 4096, 512), (7, 96, 33), (64, 1001, 257),
-                                           (17, 3, 5), (40, 130, 16)])
+                                           (17, 3, 5), (40, 130, 16), (3, 2001, 100),
+                                           (5, 1030, 20)])
 def test_random_inputs_match_the_oracle(backend, rng, dtype, rows, cols, out):
     x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
     bits = weight_bits(rng.standard_normal((out, cols)), dtype)
@@ -100,23 +103,24 @@ def test_integer_inputs_are_bit_exact(backend, rng, dtype):
     assert np.array_equal(backend.linear(bits, x, dtype), O.linear(x, bits, dtype))
 
 
-def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod):
+@pytest.mark.parametrize("cols", [256, 3072])  # 3072: K split over workgroups
+def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod, cols):
     torch = torch_mod
-    x = rng.standard_normal((9, 256)).astype(np.float32)
-    bits = weight_bits(rng.standard_normal((130, 256)), BF16)
+    x = rng.standard_normal((9, cols)).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((130, cols)), BF16)
     prepared = backend.create_weight(bits, BF16)
     try:
         host = backend.linear(prepared, x)
         dx = torch.from_numpy(x).cuda()
         dy = torch.zeros((9, 130), device="cuda")
         backend.check(backend.lib.safetyraise_kernel_linear_device(
-            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, 256,
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, cols,
             C.c_void_p(dy.data_ptr()), 9, 130), "linear_device")
         backend.synchronize()
         assert np.array_equal(dy.cpu().numpy(), host)
         # the same shape checks as linear
         assert backend.lib.safetyraise_kernel_linear_device(
-            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, 255,
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 9, cols - 1,
             C.c_void_p(dy.data_ptr()), 9, 130) == 1
     finally:
         prepared.destroy()
