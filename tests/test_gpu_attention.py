@@ -367,8 +367,11 @@ def test_capabilities_advertise_the_extension(pkg, backend):
     caps = backend.capabilities
     assert caps.abi_version == 1 and caps.struct_size >= 40
     assert caps.device_kind == 3
-    assert caps.dtype_mask == 0
+    assert caps.dtype_mask == (1 << 1) | (1 << 2) | (1 << 3)  # F32, F16, BF16 projections
     assert backend.supports(pkg.CAP_ATTENTION) and backend.supports(pkg.CAP_GDN)
+    assert np.array_equal(backend.linear(np.ones((2, 2), np.float32), np.ones((1, 2), np.float32)),
+                          np.full((1, 2), 2.0, np.float32))
+    # quantised weight formats (dtype 4 and up) stay on the engine's matmul
     with pytest.raises(pkg.PluginError) as err:
-        backend.linear(np.ones((2, 2), np.float32), np.ones((1, 2), np.float32))
+        backend.create_weight(np.ones((2, 2), np.uint16), 4)
     assert err.value.status == 2
