@@ -11,17 +11,19 @@
 // of K; its four waves take quarters of that range and meet in LDS.
 // Decode-sized calls (M <= 16) thus stream every weight row once, which is
 // the HBM-bound regime the ABI's projections live in; each k-step loads 16
-// bytes of x and 4 weight elements per lane and feeds 4 MFMAs.  A call with
+// bytes of x and 8 weight elements per lane and feeds 8 MFMAs.  A call with
 // fewer tiles than kLinWgPerCu workgroups per CU splits K over up to
 // kLinMaxSplits workgroups per tile (grid z): those write partial sums and
 // a second kernel adds them in split order, so results do not depend on
 // timing.
 //
-// Operand order.  For MFMA t of a 16-wide k block, lane (r = lane % 16,
-// g = lane / 16) feeds A = x[row r][k0 + 4g + t] and B = W[output r][same k]:
-// the four MFMAs cover the block's 16 k values with each lane reading 4
-// consecutive ones (any order of k gives the same sum; A and B share it).
-// The accumulator then holds y[row 4g + i][output r] in element i.
+// Operand order.  For MFMA t of a 32-wide k block, lane (r = lane % 16,
+// g = lane / 16) feeds A = x[row r][k0 + 8g + t] and B = W[output r][same k]:
+// the eight MFMAs cover the block's 32 k values with each lane reading 8
+// consecutive ones (any order of k gives the same sum; A and B share it), so
+// the four lanes of a row read 128 contiguous bytes of x and 64 of a bf16
+// weight row per block.  The accumulator then holds y[row 4g + i][output r]
+// in element i.
 
 #include <algorithm>
 
@@ -32,13 +34,15 @@ namespace sr {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kLinTile = 16;   // rows and outputs per workgroup
 constexpr int kLinWaves = 4;   // waves splitting K
 constexpr uint32_t kLinWgPerCu = 1;    // workgroups per CU a call aims for
 constexpr uint32_t kLinMaxSplits = 8;  // K splits per tile at most
-constexpr uint32_t kLinMinSplitK = 512;  // K per split at least (8 blocks per wave)
+constexpr uint32_t kLinBlock = 32;      // k per block (8 MFMAs)
+constexpr uint32_t kLinMinSplitK = 512;  // K per split at least (4 blocks per wave)
 
 template <int DT>
 __device__ __forceinline__ float widen(const void *w, size_t i) {
@@ -51,32 +55,37 @@ __device__ __forceinline__ float widen(const void *w, size_t i) {
     }
 }
 
-// Elements k .. k+3 of a row starting at element `row`, those from `lim` on
+// Elements k .. k+7 of a row starting at element `row`, those from `lim` on
 // replaced by 0.  The reads themselves are clamped into the row (K >= 1;
-// kVec: K a multiple of 4), and the zeros are selected after the load: a
-// load behind a branch would make later waits wait for every load in flight.
-// kVec: the row start is 16-byte aligned for f32 (8-byte for 16-bit weights).
+// kVec: K a multiple of 8, so k and lim are too), and the zeros are selected
+// after the load: a load behind a branch would make later waits wait for
+// every load in flight.  kVec: the row start is 32-byte aligned for f32
+// (16-byte for 16-bit weights).
 template <int DT, bool kVec>
-__device__ __forceinline__ f32x4 load4(const void *base, size_t row, uint32_t k, uint32_t K,
+__device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k, uint32_t K,
                                        uint32_t lim) {
-    f32x4 v;
+    f32x8 v;
     if constexpr (kVec) {
-        const size_t i = row + min(k, K - 4);
+        const size_t i = row + min(k, K - 8);
         if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F32) {
-            v = *(const f32x4 *)((const float *)base + i);
+            const f32x4 lo = *(const f32x4 *)((const float *)base + i);
+            const f32x4 hi = *(const f32x4 *)((const float *)base + i + 4);
+            v = f32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         } else if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F16) {
-            v = __builtin_convertvector(*(const f16x4 *)((const _Float16 *)base + i), f32x4);
+            v = __builtin_convertvector(*(const f16x8 *)((const _Float16 *)base + i), f32x8);
         } else {
-            const uint2 u = *(const uint2 *)((const uint16_t *)base + i);
-            v = f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u)};
+            const uint4 u = *(const uint4 *)((const uint16_t *)base + i);
+            v = f32x8{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u),
+                      __uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                      __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
         }
         const bool live = k < lim;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = live ? v[j] : 0.0f;
+        for (int j = 0; j < 8; ++j) v[j] = live ? v[j] : 0.0f;
     } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 8; ++j) {
             const float e = widen<DT>(base, row + min(k + j, K - 1));
             v[j] = k + j < lim ? e : 0.0f;
         }
@@ -108,45 +117,45 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     const size_t xrow = (size_t)min(m0 + r, M - 1) * K;
     const size_t wrow = (size_t)min(n0 + r, N - 1) * K;
     y += (size_t)blockIdx.z * M * N;
-    const uint32_t nblk = (K + 15) / 16;
+    const uint32_t nblk = (K + kLinBlock - 1) / kLinBlock;
     const uint32_t s0 = (uint32_t)((uint64_t)nblk * blockIdx.z / gridDim.z);
     const uint32_t s1 = (uint32_t)((uint64_t)nblk * (blockIdx.z + 1) / gridDim.z);
     const uint32_t b0 = s0 + (uint32_t)((uint64_t)(s1 - s0) * wave / kLinWaves);
     const uint32_t b1 = s0 + (uint32_t)((uint64_t)(s1 - s0) * (wave + 1) / kLinWaves);
     // this wave's k range ends at kend: loads past it read zeros, so a group
     // that runs past the range adds nothing (and no block is counted twice)
-    const uint32_t kend = min(16 * b1, K);
+    const uint32_t kend = min(kLinBlock * b1, K);
     // groups of kGroup blocks in two register sets: while the MFMAs of one
     // set run, the loads of the other are in flight (the sets alternate
     // explicitly, so the compiler cannot merge them into one and wait for
     // loads it has just issued)
-    constexpr int kGroup = 8;
-    f32x4 xa[kGroup], wa[kGroup], xb[kGroup], wb[kGroup];
-    auto load_group = [&](uint32_t b, f32x4 (&xv)[kGroup], f32x4 (&wv)[kGroup])
+    constexpr int kGroup = 4;
+    f32x8 xa[kGroup], wa[kGroup], xb[kGroup], wb[kGroup];
+    auto load_group = [&](uint32_t b, f32x8 (&xv)[kGroup], f32x8 (&wv)[kGroup])
                           __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kGroup; ++j) {
-            const uint32_t k = 16 * (b + j) + 4 * g;
-            xv[j] = load4<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K, kend);
-            wv[j] = load4<DT, kVec>(w, wrow, k, K, kend);
+            const uint32_t k = kLinBlock * (b + j) + 8 * g;
+            xv[j] = load8<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K, kend);
+            wv[j] = load8<DT, kVec>(w, wrow, k, K, kend);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    // four accumulation chains (block j of a group feeds chain j % 4), so
+    // four accumulation chains (MFMA t of a block feeds chain t % 4), so
     // consecutive MFMAs do not wait for each other's results
     constexpr int kChains = 4;
     f32x4 acc4[kChains];
 #pragma unroll
     for (int c = 0; c < kChains; ++c) acc4[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mfma_group = [&](const f32x4 (&xv)[kGroup], const f32x4 (&wv)[kGroup])
+    auto mfma_group = [&](const f32x8 (&xv)[kGroup], const f32x8 (&wv)[kGroup])
                           __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kGroup; ++j) {
-            f32x4 &a = acc4[j % kChains];
-            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].x, wv[j].x, a, 0, 0, 0);
-            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].y, wv[j].y, a, 0, 0, 0);
-            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].z, wv[j].z, a, 0, 0, 0);
-            a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j].w, wv[j].w, a, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                f32x4 &a = acc4[t % kChains];
+                a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][t], wv[j][t], a, 0, 0, 0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -192,7 +201,7 @@ template <int DT>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
                uint32_t K, uint32_t splits) {
     const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile, splits);
-    if ((K & 3u) == 0) {
+    if ((K & 7u) == 0) {
         hipLaunchKernelGGL((linear_kernel<DT, true>), grid, dim3(64 * kLinWaves), 0, stream, x, w, y,
                            M, N, K);
     } else {
