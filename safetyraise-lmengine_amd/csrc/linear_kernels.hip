@@ -93,8 +93,10 @@ __device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k,
     return v;
 }
 
-// y: the output, or (grid z > 1) partial sums [grid z][M][N]
-template <int DT, bool kVec>
+// y: the output, or (grid z > 1) partial sums [grid z][M][N].  kGroup: k
+// blocks per register set (4; 2 for calls with many workgroups per CU, which
+// then hold more waves per SIMD).
+template <int DT, bool kVec, int kGroup>
 __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, const void *w,
                                                                  float *y, uint32_t M, uint32_t N,
                                                                  uint32_t K) {
@@ -129,7 +131,6 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     // set run, the loads of the other are in flight (the sets alternate
     // explicitly, so the compiler cannot merge them into one and wait for
     // loads it has just issued)
-    constexpr int kGroup = 4;
     f32x8 xa[kGroup], wa[kGroup], xb[kGroup], wb[kGroup];
     auto load_group = [&](uint32_t b, f32x8 (&xv)[kGroup], f32x8 (&wv)[kGroup])
                           __attribute__((always_inline)) {
@@ -197,16 +198,28 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
     y[i] = s;
 }
 
-template <int DT>
+template <int DT, int kGroup>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
                uint32_t K, uint32_t splits) {
     const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile, splits);
     if ((K & 7u) == 0) {
-        hipLaunchKernelGGL((linear_kernel<DT, true>), grid, dim3(64 * kLinWaves), 0, stream, x, w, y,
+        hipLaunchKernelGGL((linear_kernel<DT, true, kGroup>), grid, dim3(64 * kLinWaves), 0, stream, x, w, y,
                            M, N, K);
     } else {
-        hipLaunchKernelGGL((linear_kernel<DT, false>), grid, dim3(64 * kLinWaves), 0, stream, x, w,
+        hipLaunchKernelGGL((linear_kernel<DT, false, kGroup>), grid, dim3(64 * kLinWaves), 0, stream, x, w,
                            y, M, N, K);
+    }
+}
+
+template <int DT>
+void launch_dt_groups(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M,
+                      uint32_t N, uint32_t K, uint32_t splits, int num_cus) {
+    const uint64_t wgs = (uint64_t)((N + kLinTile - 1) / kLinTile) * ((M + kLinTile - 1) / kLinTile) *
+                         splits;
+    if (wgs >= 2 * (uint64_t)(num_cus > 0 ? num_cus : 1)) {
+        launch_dt<DT, 2>(stream, x, w, y, M, N, K, splits);
+    } else {
+        launch_dt<DT, 4>(stream, x, w, y, M, N, K, splits);
     }
 }
 
@@ -237,13 +250,13 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
     float *dst = splits > 1 ? scratch : y;
     switch (dtype) {
         case SAFETYRAISE_KERNEL_DTYPE_F32:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, dst, M, N, K, splits);
+            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, dst, M, N, K, splits, num_cus);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_F16:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, dst, M, N, K, splits);
+            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, dst, M, N, K, splits, num_cus);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_BF16:
-            launch_dt<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, dst, M, N, K, splits);
+            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, dst, M, N, K, splits, num_cus);
             break;
         default:
             return hipErrorInvalidValue;

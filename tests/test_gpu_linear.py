@@ -8,7 +8,9 @@ reordered f32 sum scales with the magnitude of the terms, not of the result),
 and integer-valued inputs, whose every partial sum is exact in f32, must match
 the oracle bit for bit.  Calls with few output tiles split K over several
 workgroups whose partial sums a second kernel adds (shapes (1, 4096, 512),
-(3, 2001, 100), (5, 1030, 20) and the 3072-column device call do).
+(3, 2001, 100), (5, 1030, 20) and the 3072-column device call do); calls with
+at least two workgroups per CU ((16, 512, 8192), (32, 130, 4100)) keep two k
+blocks per register set instead of four.
 """
 import ctypes as C
 
@@ -82,7 +84,7 @@ def test_known_answer_capabilities_and_errors(pkg, backend):
 @pytest.mark.parametrize("dtype", [F32, F16, BF16])
 @pytest.mark.parametrize("rows,cols,out", [(1, 4096, 512), (7, 96, 33), (64, 1001, 257),
                                            (17, 3, 5), (40, 130, 16), (3, 2001, 100),
-                                           (5, 1030, 20)])
+                                           (5, 1030, 20), (16, 512, 8192), (32, 130, 4100)])
 def test_random_inputs_match_the_oracle(backend, rng, dtype, rows, cols, out):
     x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
     bits = weight_bits(rng.standard_normal((out, cols)), dtype)
