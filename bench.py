@@ -10,10 +10,14 @@ independent caches).  Inputs and caches are resident in HBM before timing.
 
 `value` is algorithmic HBM bytes per step / step time.  `roofline` is for
 the dominant kernel (attn_decode_kernel<128,4>): algorithmic bytes per launch
-/ its average launch duration measured with HIP events on the stream the
-plugin launches on.  `cpu_baseline` times the CPU oracle (the C restatement
-of the reference's src/model/math.rs) on the same cache contents, one layer,
-on the host cores of this machine.
+/ its average launch duration, measured in a second pass with the plugin's
+kernel timing (HIP start/stop events of each dispatch, recorded on the stream
+the plugin launches on); `kernels` lists every kernel of that pass with its
+launches per call and mean duration.  `cpu_baseline` times the CPU oracle
+(the C restatement of the reference's src/model/math.rs) on the same cache
+contents, one layer, on the host cores of this machine.  The other workloads
+on the line (prefill, verify, gdn_decode, gdn_prefill, linear) are measured
+the same way.
 """
 from __future__ import annotations
 
@@ -63,6 +67,22 @@ def traffic_from_profiles(kernel_tag: str):
         return json.loads(f.read_text()).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
+
+
+def kernel_pass(backend, run, calls):
+    """Runs `run()` (which makes `calls` plugin calls) with the plugin's kernel
+    timing on: each launch's device duration from the start/stop timestamps of
+    its own dispatch (hipExtLaunchKernelGGL events on the plugin's stream), the
+    figure a profiler's kernel trace records.  Returns {kernel name:
+    {"per_call": launches per call, "us": mean duration}}."""
+    backend.timing(True)
+    try:
+        run()
+        times = backend.kernel_times()
+    finally:
+        backend.timing(False)
+    return {name: {"per_call": round(n / calls, 3), "us": round(us, 2)}
+            for name, (n, us) in times.items()}
 
 
 def bench_decode(args, torch, pkg):
@@ -143,8 +163,6 @@ def bench_decode(args, torch, pkg):
                 backend.check(st, "attention_forward")
     backend.synchronize()
 
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps * layers)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -158,26 +176,24 @@ def bench_decode(args, torch, pkg):
     torch.cuda.synchronize()
     backend.synchronize()
     total_ms = t0.elapsed_time(t1)
-    # per-call durations in a second pass of the same number of steps (event
-    # markers between calls stall the queue, so they stay out of the timed
-    # region); each call there sees `steps` more keys per sequence
-    i = 0
-    for s in range(total_steps, event_steps):
-        for l in range(layers):
-            ev[i][0].record(stream)
-            st = fwd(ctx, C.byref(all_args[s][l]))
-            ev[i][1].record(stream)
-            i += 1
-            if st != 0:
-                backend.check(st, "attention_forward")
-    torch.cuda.synchronize()
-    backend.synchronize()
+    # kernel durations in a second pass of the same number of steps (the
+    # timing events stay out of the timed region); each call there sees
+    # `steps` more keys per sequence
+
+    def second_pass():
+        for s in range(total_steps, event_steps):
+            for l in range(layers):
+                st = fwd(ctx, C.byref(all_args[s][l]))
+                if st != 0:
+                    backend.check(st, "attention_forward")
+
+    kernels = kernel_pass(backend, second_pass, args.steps * layers)
     ms_per_step = total_ms / args.steps
     bytes_total = sum(step_bytes(s) for s in range(args.warmup, total_steps)) * layers
     value = bytes_total / (total_ms * 1e-3) / 1e9
-    launch_us = np.array([a.elapsed_time(b) * 1e3 for a, b in ev])
+    launch_us = kernels["attn_decode_kernel"]["us"]
     per_launch_bytes = sum(step_bytes(s) for s in range(total_steps, event_steps)) / args.steps
-    achieved = per_launch_bytes / (launch_us.mean() * 1e-6) / 1e9
+    achieved = per_launch_bytes / (launch_us * 1e-6) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -211,12 +227,13 @@ def bench_decode(args, torch, pkg):
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("attn_decode_qwen3_8b"),
-            # one decode call = the split-K kernel plus its small combine pass;
-            # the events bracket both (rocprofv3 lists them separately)
-            "kernel": "attn_decode_kernel<128,4> + attn_combine_kernel<128,4>",
-            "launch_us_mean": round(float(launch_us.mean()), 2),
+            # the split-K kernel reads every cached K/V byte; its small
+            # combine pass merges the per-slice records (listed in `kernels`)
+            "kernel": "attn_decode_kernel<128,4,true>",
+            "launch_us_mean": round(float(launch_us), 2),
             "bytes_per_launch": int(per_launch_bytes),
         },
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
     for p in pools:
@@ -330,23 +347,17 @@ def bench_prefill(args, torch, pkg, steps, warmup):
 
     step_flops = sum(chunk_flops(c) for c in range(nchunk))
 
-    def run_step(events=None):
+    def run_step():
         for s in ids:
             pool.truncate(s, 0)
         for c in range(nchunk):
-            if events is not None:
-                events[c][0].record(stream)
             st = fwd(ctx, C.byref(chunk_args[c]))
-            if events is not None:
-                events[c][1].record(stream)
             if st != 0:
                 backend.check(st, "attention_forward")
 
     for _ in range(warmup):
         run_step()
     backend.synchronize()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(nchunk)] for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -357,19 +368,20 @@ def bench_prefill(args, torch, pkg, steps, warmup):
     torch.cuda.synchronize()
     backend.synchronize()
     total_ms = t0.elapsed_time(t1)
-    # per-call durations (the roofline's launch figure) come from a second
-    # pass: event markers between calls stall the queue for a few us each, so
-    # they stay out of the timed region; one unrecorded step queued first
-    # brings the GPU back from idle
+    # kernel durations (the roofline's launch figure) come from a second pass
+    # with the plugin's kernel timing on; one untimed step queued first brings
+    # the GPU back from idle
     run_step()
-    for s in range(steps):
-        run_step(ev[s])
-    torch.cuda.synchronize()
-    backend.synchronize()
+
+    def second_pass():
+        for s in range(steps):
+            run_step()
+
+    kernels = kernel_pass(backend, second_pass, steps * nchunk)
     ms_per_step = total_ms / steps
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
-    per_chunk_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev]).mean(0)
-    call_tflops = step_flops / (per_chunk_us.sum() * 1e-6) / 1e12
+    attn_us = kernels["attn_prefill_pp_kernel"]["us"]
+    call_tflops = step_flops / nchunk / (attn_us * 1e-6) / 1e12
     result = {
         "workload": "qwen3-8b chunked causal prefill attention (BASELINE config 3): 4 x 4096 "
                     "tokens in chunks of 512, one layer per step",
@@ -379,8 +391,10 @@ def bench_prefill(args, torch, pkg, steps, warmup):
         "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms_per_step, 4),
         "gflop_per_step": round(step_flops / 1e9, 2),
-        "dtype": "bf16 MFMA, f32 accumulate and softmax",
-        "chunk_us": [round(float(x), 1) for x in per_chunk_us],
+        # K and V are the cache's bf16 values converted exactly to fp16 while
+        # staged; q and P are rounded to fp16 (the fp16 MFMA has the bf16 rate)
+        "dtype": "fp16 MFMA operands (v_mfma_f32_32x32x16_f16) over the bf16 cache, "
+                 "f32 accumulate and softmax",
         "roofline": {
             "bound": "mfma",
             "achieved": round(call_tflops, 2),
@@ -388,10 +402,12 @@ def bench_prefill(args, torch, pkg, steps, warmup):
             "unit": "TFLOP/s",
             "frac": round(call_tflops / MFMA_BF16_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("attn_prefill_qwen3_8b"),
-            "kernel": "kv_append_rows_kernel<128> + attn_prefill_kernel<128,4>",
-            "launch_us_mean": round(float(per_chunk_us.mean()), 2),
+            "kernel": "attn_prefill_pp_kernel<128,4,true>",
+            "launch_us_mean": round(float(attn_us), 2),
+            "flops_per_launch": int(step_flops // nchunk),
             "flops_per_step": int(step_flops),
         },
+        "kernels": kernels,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim,
@@ -505,21 +521,15 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
     fwd = backend.lib.safetyraise_kernel_gdn_forward
     ctx = backend.context
 
-    def run(step, events=None):
+    def run(step):
         for l in range(layers):
-            if events is not None:
-                events[l][0].record(stream)
             st = fwd(ctx, C.byref(all_args[l][step & 1]))
-            if events is not None:
-                events[l][1].record(stream)
             if st != 0:
                 backend.check(st, "gdn_forward")
 
     for s in range(warmup):
         run(s)
     backend.synchronize()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(layers)] for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -529,13 +539,15 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
     t1.record(stream)
     torch.cuda.synchronize()
     backend.synchronize()
-    # per-call durations in a second pass, outside the timed region, after
-    # one unrecorded step
+    # kernel durations in a second pass, outside the timed region, after one
+    # untimed step
     run(warmup + steps)
-    for s in range(steps):
-        run(warmup + steps + 1 + s, ev[s])
-    torch.cuda.synchronize()
-    backend.synchronize()
+
+    def second_pass():
+        for s in range(steps):
+            run(warmup + steps + 1 + s)
+
+    kernels = kernel_pass(backend, second_pass, steps * layers)
     C_ = 2 * hk * dk + hv * dv
     per_layer = (2 * nseq * hv * dv * dk * 4          # state read + write
                  + 2 * nseq * C_ * (K - 1) * 4        # conv history read + write
@@ -543,9 +555,10 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
                  + C_ * K * 4                         # conv weights
                  + nseq * hv * dv * 4)                # output
     ms = t0.elapsed_time(t1) / steps
-    call_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev])
+    head_name = next(n for n in kernels if n.startswith("gdn_head"))
+    call_us = kernels[head_name]["us"]
     value = per_layer * layers / (ms * 1e-3) / 1e9
-    achieved = per_layer / (call_us.mean() * 1e-6) / 1e9
+    achieved = per_layer / (call_us * 1e-6) / 1e9
     result = {
         "workload": f"qwen3.5 GDN decode (BASELINE config 4): Hk 16 / Hv 32, d 128, conv 4, "
                     f"batch 8, {layers} layers per step",
@@ -558,9 +571,10 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("gdn_decode_qwen35"),
             "kernel": "gdn_head_kernel<512, ConvK<4>>",
-            "launch_us_mean": round(float(call_us.mean()), 2),
+            "launch_us_mean": round(float(call_us), 2),
             "bytes_per_launch": int(per_layer),
         },
+        "kernels": kernels,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_gdn(pools[0][0], pools[0][1], pools[0][3][0],
@@ -615,13 +629,9 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         state["ids"] = [pool.open() for _ in range(nseq)]
         state["args"] = make(state["ids"])
 
-    def run(events=None):
+    def run():
         for c in range(nchunk):
-            if events is not None:
-                events[c][0].record(stream)
             st = fwd(ctx, C.byref(state["args"][c]))
-            if events is not None:
-                events[c][1].record(stream)
             if st != 0:
                 backend.check(st, "gdn_forward")
 
@@ -629,8 +639,6 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         reset()
         run()
     backend.synchronize()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(nchunk)] for _ in range(steps)]
     total_ms = 0.0
     for s in range(steps):
         reset()  # host bookkeeping and a state clear, outside the timed region
@@ -644,40 +652,46 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         torch.cuda.synchronize()
         total_ms += t0.elapsed_time(t1)
     backend.synchronize()
-    # per-call durations in a second pass, outside the timed region (event
-    # markers between calls stall the queue)
-    for s in range(steps):
-        reset()
-        backend.synchronize()
-        run(ev[s])
-        torch.cuda.synchronize()
-    backend.synchronize()
+    # kernel durations in a second pass, outside the timed region
+
+    def second_pass():
+        for s in range(steps):
+            reset()
+            run()
+
+    kernels = kernel_pass(backend, second_pass, steps * nchunk)
     ms = total_ms / steps
     flops = 7 * dk * dv * hv * nseq * total
     tflops = flops / (ms * 1e-3) / 1e12
-    call_us = np.array([[a.elapsed_time(b) * 1e3 for a, b in row] for row in ev])
-    call_tf = flops / (call_us.sum(1).mean() * 1e-6) / 1e12
-    ck = 32  # rows per chunk of the kernel
+    # the roofline's algorithmic count: the chunked (WY) form's FLOPs at the
+    # call's chunk of C = 64 rows, 4 C^2 Dk + 2/3 C^3 + 4 C^2 Dv + 8 C Dk Dv +
+    # 2 C^2 Dv per (sequence, value head, chunk); the token-serial count is
+    # reported beside it
+    ck = chunk
     chunked_form = ((4 * ck * ck * dk + 2 * ck ** 3 / 3 + 4 * ck * ck * dv + 8 * ck * dk * dv
                      + 2 * ck * ck * dv) * nseq * hv * (total // ck))
-    chunk_tf = chunked_form / (call_us.sum(1).mean() * 1e-6) / 1e12
+    chunk_us = kernels["gdn_chunk_kernel"]["us"]
+    chunk_tf = chunked_form / nchunk / (chunk_us * 1e-6) / 1e12
+    serial_tf = flops / nchunk / (chunk_us * 1e-6) / 1e12
     result = {
         "workload": "qwen3.5 GDN prefill (BASELINE config 4): 2 x 2048 tokens in chunks of 64, "
                     "one layer per step, from a zero state",
         "value": round(tflops, 3), "unit": "TFLOP/s",
-        "token_serial_tflops_per_launch": round(call_tf, 3),
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
         "gflop_per_step_token_serial": round(flops / 1e9, 2),
         "gflop_per_step_chunked_form": round(chunked_form / 1e9, 2),
-        "dtype": "f32 (MFMA 16x16x4 f32, chunked WY form, C = 32)",
+        "dtype": "f32 (MFMA 16x16x4 f32, chunked WY form)",
         "roofline": {
             "bound": "mfma", "achieved": round(chunk_tf, 3), "peak": MFMA_F32_PEAK_TFS,
             "unit": "TFLOP/s", "frac": round(chunk_tf / MFMA_F32_PEAK_TFS, 4),
+            "frac_token_serial": round(serial_tf / MFMA_F32_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("gdn_prefill_qwen35"),
-            "kernel": "gdn_chunk_kernel + gdn_norm_gate_kernel",
-            "launch_us_mean": round(float(call_us.mean()), 2),
+            "kernel": "gdn_chunk_kernel<ConvK<4>>",
+            "launch_us_mean": round(float(chunk_us), 2),
+            "flops_per_launch": int(chunked_form / nchunk),
             "flops_per_step": int(chunked_form),
         },
+        "kernels": kernels,
     }
     if not args.no_cpu:
         ids_c = (C.c_uint32 * nseq)(*state["ids"])
@@ -748,14 +762,11 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
     fn = backend.lib.safetyraise_kernel_linear_device
     ctx = backend.context
 
-    def run(events=None):
-        for i, (out_f, in_f) in enumerate(LINEAR_SHAPES):
-            if events is not None:
-                events[i][0].record(stream)
+    def run(which=range(len(LINEAR_SHAPES))):
+        for i in which:
+            out_f, in_f = LINEAR_SHAPES[i]
             st = fn(ctx, weights[i].handle, C.c_void_p(xs[i].data_ptr()), rows, in_f,
                     C.c_void_p(ys[i].data_ptr()), rows, out_f)
-            if events is not None:
-                events[i][1].record(stream)
             if st != 0:
                 backend.check(st, "linear_device")
 
@@ -772,20 +783,18 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
     torch.cuda.synchronize()
     backend.synchronize()
     run()
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in LINEAR_SHAPES] for _ in range(steps)]
-    for s in range(steps):
-        run(ev[s])
-    torch.cuda.synchronize()
+    # kernel durations in second passes: every call (the breakdown), then the
+    # dominant call shape alone for the roofline, gate/up (12288 x 4096)
+    kernels = kernel_pass(backend, lambda: [run() for _ in range(steps)],
+                          steps * len(LINEAR_SHAPES))
+    big = [4, 5]
+    big_kernels = kernel_pass(backend, lambda: [run(big) for _ in range(steps)], steps * len(big))
     per_call = [o * i * 2 + rows * (i + o) * 4 for o, i in LINEAR_SHAPES]
     per_step = sum(per_call)
     ms = t0.elapsed_time(t1) / steps
     value = per_step / (ms * 1e-3) / 1e9
-    # the dominant call shape for the roofline: gate/up (12288 x 4096)
-    big = [4, 5]
-    big_us = np.array([[ev[s][i][0].elapsed_time(ev[s][i][1]) * 1e3 for i in big]
-                       for s in range(steps)])
-    achieved = per_call[4] / (big_us.mean() * 1e-6) / 1e9
+    big_us = big_kernels["linear_kernel"]["us"]
+    achieved = per_call[4] / (big_us * 1e-6) / 1e9
     result = {
         "workload": f"Qwen3-8B decoder-layer projections (q/k/v/o/gate/up/down, bf16 weights, "
                     f"386 MB), {rows} rows, f32 in/out, device pointers",
@@ -798,9 +807,10 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("linear_qwen3_8b"),
             "kernel": "linear_kernel<BF16> (12288 x 4096 gate/up calls)",
-            "launch_us_mean": round(float(big_us.mean()), 2),
+            "launch_us_mean": round(float(big_us), 2),
             "bytes_per_launch": int(per_call[4]),
         },
+        "kernels": kernels,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_linear(weights[0], xs[0], rows)
@@ -830,14 +840,15 @@ def cpu_baseline_linear(weight, x_dev, rows):
             "ms": round(t * 1e3, 2)}
 
 
-def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
+def bench_verify(args, torch, pkg, steps, warmup, rows=5):
     """long-context MTP speculative-verify attention, Qwen3-32B
     shape: 64 Q / 8 KV heads, head_dim 128, 1 + 4 draft rows per sequence (row j
     sees 131072 + j + 1 keys), batch 4, context 131072, paged bf16 KV in 16-token
-    pages whose order interleaves the four sequences at random.  One step = one
-    verify call; the drafts are truncated away afterwards (the next step verifies
-    at the same context).  Inputs ~N(0,1) are taken as normalised (no QK-norm);
-    RoPE is applied as part of the fused path."""
+    pages whose ids are a seeded random permutation of the pool (the pool's
+    page_order_seed), so no two consecutive pages of a sequence are adjacent
+    except by chance.  One step = one verify call; the drafts are truncated away
+    afterwards (the next step verifies at the same context).  Inputs ~N(0,1) are
+    taken as normalised (no QK-norm); RoPE is applied as part of the fused path."""
     heads, kvh, dim, nseq, ctx_len, page = 64, 8, 128, 4, 131072, 16
     backend = pkg.NativeBackend.load()
     stream = torch.cuda.Stream()
@@ -845,24 +856,14 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
     backend.set_stream(stream.cuda_stream)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x5A5A0005)
-    rng = np.random.default_rng(0x5A5A0005)
     max_tokens = ctx_len + rows + 16
     pool = pkg.KvCache(backend, kvh, dim, page, nseq * (max_tokens // page + 2) + 8, max_tokens,
-                       nseq)
+                       nseq, page_order_seed=0x5A5A0005)
     ids = [pool.open() for _ in range(nseq)]
-    # fill in random-length runs of whole pages, sequences in random order,
-    # so each sequence's pages are spread over the pool
     kfull = torch.randn((ctx_len, kvh * dim), generator=gen, device="cuda", dtype=torch.bfloat16)
     vfull = torch.randn((ctx_len, kvh * dim), generator=gen, device="cuda", dtype=torch.bfloat16)
-    filled = [0] * nseq
-    while min(filled) < ctx_len:
-        order = [i for i in range(nseq) if filled[i] < ctx_len]
-        rng.shuffle(order)
-        for i in order:
-            n = min(page * int(rng.integers(1, 9)) if interleave else ctx_len, ctx_len - filled[i])
-            pool.append(ids[i], kfull[filled[i]:filled[i] + n], vfull[filled[i]:filled[i] + n],
-                        flags=pkg.ASYNC)
-            filled[i] += n
+    for s_ in ids:
+        pool.append(s_, kfull, vfull, flags=pkg.ASYNC)
     backend.synchronize()
     del kfull, vfull
     q = torch.randn((nseq * rows, heads * dim), generator=gen, device="cuda")
@@ -887,12 +888,8 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
     fwd = backend.lib.safetyraise_kernel_attention_forward
     ctx = backend.context
 
-    def run(events=None):
-        if events is not None:
-            events[0].record(stream)
+    def run():
         st = fwd(ctx, C.byref(a))
-        if events is not None:
-            events[1].record(stream)
         if st != 0:
             backend.check(st, "attention_forward")
         for s_ in ids:
@@ -901,8 +898,6 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
     for _ in range(warmup):
         run()
     backend.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -913,24 +908,26 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
     torch.cuda.synchronize()
     backend.synchronize()
     ms = t0.elapsed_time(t1) / steps
-    # per-call durations in a second pass (event markers between calls stall
-    # the queue, so they stay out of the timed region), after two unrecorded
-    # calls that bring the GPU back from idle
+    # kernel durations in a second pass (outside the timed region), after two
+    # untimed calls that bring the GPU back from idle
     run()
     run()
-    for s_ in range(steps):
-        run(ev[s_])
-    torch.cuda.synchronize()
-    backend.synchronize()
-    call_us = np.array([x.elapsed_time(y) * 1e3 for x, y in ev])
+
+    def second_pass():
+        for _ in range(steps):
+            run()
+
+    kernels = kernel_pass(backend, second_pass, steps)
+    call_us = kernels["attn_verify_kernel"]["us"]
     keys = sum(ctx_len + j + 1 for j in range(rows))  # per sequence, summed over rows
     nbytes = nseq * (ctx_len + rows) * kvh * dim * 2 * 2
     flops = nseq * heads * 4 * dim * keys
     gbs = nbytes / (ms * 1e-3) / 1e9
-    achieved = nbytes / (call_us.mean() * 1e-6) / 1e9
+    achieved = nbytes / (call_us * 1e-6) / 1e9
     result = {
         "workload": "qwen3-32b MTP verify attention (BASELINE config 5): 64 Q / 8 KV heads, "
-                    "d 128, 1 + 4 rows, batch 4, context 131072, 16-token pages interleaved",
+                    "d 128, 1 + 4 rows, batch 4, context 131072, 16-token pages in a random "
+                    "permutation of the pool",
         "value": round(gbs, 2), "unit": "GB/s",
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
@@ -940,11 +937,11 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5, interleave=True):
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles("attn_verify_qwen3_32b"),
-            "kernel": "kv_append_rows_kernel<128> + attn_verify_kernel<128> + "
-                      "attn_verify_combine_kernel<128>",
-            "launch_us_mean": round(float(call_us.mean()), 2),
+            "kernel": "attn_verify_kernel<128>",
+            "launch_us_mean": round(float(call_us), 2),
             "bytes_per_launch": int(nbytes),
         },
+        "kernels": kernels,
     }
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_verify(pool, ids[0], q, k, v, pos, heads, kvh, dim,

@@ -33,7 +33,10 @@
  * SAFETYRAISE_MI355X_ASYNC is set (device pointers only): the work is then
  * enqueued on the context stream, and errors the kernels detect (non-finite
  * K/V or norm variance, as the reference rejects them) are reported by the
- * next synchronous call or by safetyraise_kernel_synchronize.
+ * next synchronous attention or GDN call, before that call changes anything,
+ * or by safetyraise_kernel_synchronize.  The asynchronous call has already
+ * advanced its sequences by then: to repeat it, kv_truncate them to their
+ * earlier lengths first.
  */
 #ifndef SAFETYRAISE_MI355X_H
 #define SAFETYRAISE_MI355X_H
@@ -76,6 +79,22 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_set_stream(
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_synchronize(
     safetyraise_kernel_context *context);
 
+/* Kernel timing, for benchmarks (no counterpart in the reference).
+ * enable != 0 waits for the context stream, clears earlier records and makes
+ * every later kernel launch of this context record its device start and end
+ * (the timestamps of the dispatch packet, as a profiler's kernel trace sees
+ * them); enable == 0 stops and frees the records.  Recording costs one event
+ * pair per launch, so timed calls are not the fastest. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_timing_enable(
+    safetyraise_kernel_context *context, uint32_t enable);
+/* Waits for the context stream, then reports the index-th distinct kernel
+ * name recorded (in order of first launch): the name (static storage), its
+ * launches and their summed device milliseconds.  INVALID_ARGUMENT past the
+ * last name. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_timing_read(
+    safetyraise_kernel_context *context, uint32_t index, const char **out_name,
+    uint64_t *out_launches, double *out_total_ms);
+
 /* ------------------------------------------------------------------------
  * Paged bf16 KV cache — replaces PagedKvCache (src/engine/state.rs:19-127).
  *
@@ -97,7 +116,11 @@ typedef struct safetyraise_kernel_kv_options {
     uint64_t num_pages;     /* pages in the pool */
     uint64_t max_tokens;    /* per-sequence capacity (max_context) */
     uint32_t max_sequences; /* sequence slots */
-    uint32_t reserved;
+    /* 0: pages are handed out in pool order (a sequence appended alone gets
+     * adjacent pages).  Otherwise the free list starts as a random
+     * permutation of the pool drawn from this seed, so every sequence's pages
+     * are scattered over the pool, as in a long-running server's cache. */
+    uint32_t page_order_seed;
 } safetyraise_kernel_kv_options;
 
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_create(

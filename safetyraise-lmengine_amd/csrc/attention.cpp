@@ -33,47 +33,71 @@ struct Region {
     size_t offset;
 };
 
-float *reserve_partials(void *user, size_t bytes) {
+// The default scratch: context-owned buffers grown on demand.
+float *grow_partials(void *user, size_t bytes) {
     Ctx *ctx = (Ctx *)user;
     if (ensure_buffer(ctx, ctx->partials, bytes, false) != kOk) {
         return nullptr;
     }
     return (float *)ctx->partials.ptr;
 }
+void *grow_rope(void *user, size_t bytes) {
+    Ctx *ctx = (Ctx *)user;
+    if (ensure_buffer(ctx, ctx->rope_scratch, bytes, false) != kOk) {
+        return nullptr;
+    }
+    return ctx->rope_scratch.ptr;
+}
 
 // One launch of the decode kernels over up to kMetaPerLaunch sequences, each
 // contributing the row `row0` at cache length `ctx`.
-int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack) {
-    DecodePlanInput plan{ctx->num_cus, reserve_partials, ctx};
+int32_t run_decode_pack(Ctx *ctx, const AttnLaunch &a, const std::vector<SeqMeta> &pack,
+                        const AttnScratch &scratch) {
+    DecodePlanInput plan{ctx->num_cus, scratch.partials, scratch.user};
     const hipError_t e = launch_attn_decode(ctx->stream, a, pack.data(), (int)pack.size(), plan);
     if (e != hipSuccess) {
-        if (ctx->error.empty() || e != hipErrorOutOfMemory) {
-            return hip_fail(ctx, e, "decode attention launch");
-        }
-        return kNoMemory;  // ensure_buffer already set the text
+        // out of memory: the scratch could not be had (its provider set the text)
+        return e == hipErrorOutOfMemory ? kNoMemory : hip_fail(ctx, e, "decode attention launch");
     }
     return kOk;
 }
 
 // The first pack launched carries the call's inline page-table entries
 // (AttnLaunch::tbl_*); they are cleared once a launch has taken them.
-int32_t run_verify_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack) {
-    DecodePlanInput plan{ctx->num_cus, reserve_partials, ctx};
-    const hipError_t e = launch_attn_verify(ctx->stream, a, pack.data(), (int)pack.size(),
-                                            ctx->rope_scratch.ptr, plan);
+int32_t run_verify_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack,
+                        const AttnScratch &scratch, void *rope) {
+    DecodePlanInput plan{ctx->num_cus, scratch.partials, scratch.user};
+    const hipError_t e =
+        launch_attn_verify(ctx->stream, a, pack.data(), (int)pack.size(), rope, plan);
     a.tbl_n = 0;
     if (e != hipSuccess) {
-        if (ctx->error.empty() || e != hipErrorOutOfMemory) {
-            return hip_fail(ctx, e, "verify attention launch");
-        }
-        return kNoMemory;
+        return e == hipErrorOutOfMemory ? kNoMemory : hip_fail(ctx, e, "verify attention launch");
     }
     return kOk;
 }
 
-int32_t run_prefill_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack) {
-    const hipError_t e =
-        launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size(), ctx->rope_scratch.ptr);
+// Sends the call's page-table entries again when the call returns an error.
+// kv_prepare_append has already changed the host page lists (fresh pages, a
+// private copy of a shared partial page); an entry that was to travel in the
+// arguments of the call's first append kernel never reaches the device if
+// the call fails before that launch, and the next append into the copied
+// page would then write into the page a forked sequence still holds.
+// Writing an entry that did arrive again is harmless.
+struct TableGuard {
+    Ctx *ctx;
+    safetyraise_kernel_kv_pool *pool;
+    TableBatch &batch;
+    bool armed = true;
+    ~TableGuard() {
+        if (!armed || batch.idx.empty()) return;
+        const std::string saved = ctx->error;  // keep the call's own message
+        (void)kv_flush_table(ctx, pool, batch);
+        ctx->error = saved;
+    }
+};
+
+int32_t run_prefill_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pack, void *rope) {
+    const hipError_t e = launch_attn_prefill(ctx->stream, a, pack.data(), (int)pack.size(), rope);
     a.tbl_n = 0;
     if (e != hipSuccess) return hip_fail(ctx, e, "prefill attention launch");
     return kOk;
@@ -81,14 +105,8 @@ int32_t run_prefill_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pa
 
 }  // namespace
 
-}  // namespace sr
-
-using namespace sr;
-
-extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
-    safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args) {
-    if (context == nullptr) return kInvalid;
-    Ctx *ctx = context;
+int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args *args,
+                               const AttnScratch &scratch) {
     if (args == nullptr || args->struct_size < sizeof(safetyraise_kernel_attention_args)) {
         return fail(ctx, kInvalid, "attention args pointer or struct_size is invalid");
     }
@@ -146,6 +164,12 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         total_rows += A.seq_rows[i];
     }
     if (total_rows > INT32_MAX) return fail(ctx, kOverflow, "too many rows");
+    if (!async) {
+        // errors of earlier ASYNC work are reported before this call changes
+        // anything, so the error word it reads at its end is its own
+        const int32_t st = report_pending_async(ctx);
+        if (st != kOk) return st;
+    }
 
     const size_t esz = bf16 ? 2 : 4;
     const size_t hs = (size_t)A.head_dim * (gated ? 2 : 1);
@@ -211,12 +235,13 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     // call's page-table entries (if few) travel in the first append kernel's
     // arguments instead of a separate update launch.
     const bool prefill_ok = prefill_supported(L);
-    bool any_serial_route = false;
+    bool any_serial_route = false, any_fast_route = false;
     for (uint32_t i = 0; i < A.num_seqs; ++i) {
         const uint32_t r = A.seq_rows[i];
         const bool fast = (r >= kPrefillMinRows && prefill_ok) ||
                           (r < kPrefillMinRows && verify_supported(L, r));
         any_serial_route = any_serial_route || !fast;
+        any_fast_route = any_fast_route || fast;
     }
     std::vector<uint64_t> old_len(A.num_seqs);
     TableBatch batch;  // one page-table upload for the whole call
@@ -228,6 +253,7 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
             return st;
         }
     }
+    TableGuard table_guard{ctx, pool, batch};
     if (!any_serial_route && batch.idx.size() <= kInlineTable) {
         L.tbl_idx = batch.idx.data();
         L.tbl_val = batch.val.data();
@@ -243,9 +269,11 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     std::vector<uint8_t> serial(A.num_seqs, 1);
     uint32_t serial_rows = 0;
     bool any_prefill = false;
-    if (prefill_ok) {
-        int32_t st = ensure_buffer(ctx, ctx->rope_scratch, prefill_rope_bytes(L, total_rows), false);
-        if (st != kOk) return st;
+    // the per-row RoPE table of the verify and prefill kernels
+    void *rope = nullptr;
+    if (prefill_ok && any_fast_route) {
+        rope = scratch.rope(scratch.user, prefill_rope_bytes(L, total_rows));
+        if (rope == nullptr) return kNoMemory;
     }
     // Sequences with 2..15 rows (MTP verify drafts) take the multi-row
     // split-K kernel: every cached K/V tile is read once for all rows.
@@ -262,13 +290,13 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
             m.row0 = (uint32_t)row0[i];
             pack.push_back(m);
             if (pack.size() == (size_t)kMetaPerLaunch) {
-                int32_t st = run_verify_pack(ctx, L, pack);
+                int32_t st = run_verify_pack(ctx, L, pack, scratch, rope);
                 if (st != kOk) return st;
                 pack.clear();
             }
         }
         if (!pack.empty()) {
-            int32_t st = run_verify_pack(ctx, L, pack);
+            int32_t st = run_verify_pack(ctx, L, pack, scratch, rope);
             if (st != kOk) return st;
         }
     }
@@ -289,13 +317,13 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
             m.row0 = (uint32_t)row0[i];
             pack.push_back(m);
             if (pack.size() == (size_t)kMetaPerLaunch) {
-                int32_t st = run_prefill_pack(ctx, L, pack);
+                int32_t st = run_prefill_pack(ctx, L, pack, rope);
                 if (st != kOk) return st;
                 pack.clear();
             }
         }
         if (!pack.empty()) {
-            int32_t st = run_prefill_pack(ctx, L, pack);
+            int32_t st = run_prefill_pack(ctx, L, pack, rope);
             if (st != kOk) return st;
         }
     }
@@ -319,7 +347,7 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
                 m.rows = 1;
                 m.row0 = (uint32_t)(row0[i] + r);
                 if (!pack.empty() && pack_tokens + m.ctx + 1 > 0x7fffffffull) {
-                    int32_t st = run_decode_pack(ctx, L, pack);
+                    int32_t st = run_decode_pack(ctx, L, pack, scratch);
                     if (st != kOk) return st;
                     pack.clear();
                     pack_tokens = 0;
@@ -327,14 +355,14 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
                 pack.push_back(m);
                 pack_tokens += (uint64_t)m.ctx + 1;
                 if (pack.size() == (size_t)kMetaPerLaunch) {
-                    int32_t st = run_decode_pack(ctx, L, pack);
+                    int32_t st = run_decode_pack(ctx, L, pack, scratch);
                     if (st != kOk) return st;
                     pack.clear();
                     pack_tokens = 0;
                 }
             }
             if (!pack.empty()) {
-                int32_t st = run_decode_pack(ctx, L, pack);
+                int32_t st = run_decode_pack(ctx, L, pack, scratch);
                 if (st != kOk) return st;
             }
         }
@@ -365,6 +393,7 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
     if (!device) {
         SR_HIP(ctx, hipMemcpyAsync(A.out, L.out, out_bytes, hipMemcpyDeviceToHost, ctx->stream));
     }
+    table_guard.armed = false;  // every launch went out: the entries are on the device
     int32_t st = finish_call(ctx, async);
     if (st != kOk && !async) {
         for (uint32_t i = 0; i < A.num_seqs; ++i) {
@@ -372,4 +401,16 @@ extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forwar
         }
     }
     return st;
+}
+
+}  // namespace sr
+
+using namespace sr;
+
+extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
+    safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args) {
+    if (context == nullptr) return kInvalid;
+    TimerScope timer_scope(context);
+    const AttnScratch scratch{grow_partials, grow_rope, context};
+    return attention_forward_impl(context, args, scratch);
 }

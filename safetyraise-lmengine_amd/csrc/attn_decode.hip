@@ -739,14 +739,14 @@ hipError_t launch_dgp(hipStream_t stream, DecodeParams &prm, const DecodePlanInp
         return hipErrorOutOfMemory;
     }
     prm.partials = partials;
-    hipLaunchKernelGGL((attn_decode_kernel<D, G, kPageHoldsChunk>),
-                       dim3((uint32_t)parts * prm.kv_heads), dim3(kThreads), 0, stream, prm);
+    SR_LAUNCH("attn_decode_kernel", (attn_decode_kernel<D, G, kPageHoldsChunk>),
+              dim3((uint32_t)parts * prm.kv_heads), dim3(kThreads), 0, stream, prm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || recs == prm.nseq) {
         return e;  // every sequence in one segment: nothing to combine
     }
-    hipLaunchKernelGGL((attn_combine_kernel<D, G>), dim3(prm.nseq * prm.kv_heads, G), dim3(D), 0,
-                       stream, prm);
+    SR_LAUNCH("attn_combine_kernel", (attn_combine_kernel<D, G>), dim3(prm.nseq * prm.kv_heads, G),
+              dim3(D), 0, stream, prm);
     return hipGetLastError();
 }
 

@@ -365,9 +365,9 @@ void launch_append(hipStream_t stream, const PrefillParams &p, uint32_t max_rows
     const uint32_t waves = max_rows * quads;
     const dim3 grid((waves + 3) / 4, p.nseq);
     if (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) {
-        hipLaunchKernelGGL((kv_append_rows_kernel<D, true>), grid, dim3(256), 0, stream, p);
+        SR_LAUNCH("kv_append_rows_kernel", (kv_append_rows_kernel<D, true>), grid, dim3(256), 0, stream, p);
     } else {
-        hipLaunchKernelGGL((kv_append_rows_kernel<D, false>), grid, dim3(256), 0, stream, p);
+        SR_LAUNCH("kv_append_rows_kernel", (kv_append_rows_kernel<D, false>), grid, dim3(256), 0, stream, p);
     }
 }
 
@@ -1368,8 +1368,8 @@ hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t bloc
             if (e != hipSuccess) return e;
             configured = true;
         }
-        hipLaunchKernelGGL((attn_prefill_pp_kernel<D, G, kTilePage>), dim3(blocks), dim3(512), lds,
-                           stream, p);
+        SR_LAUNCH("attn_prefill_pp_kernel", (attn_prefill_pp_kernel<D, G, kTilePage>), dim3(blocks),
+                  dim3(512), lds, stream, p);
     } else {
         const size_t lds = 4 * kTileBytes<D>;  // K and V^T, double buffered
         if (!configured) {
@@ -1379,8 +1379,8 @@ hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t bloc
             if (e != hipSuccess) return e;
             configured = true;
         }
-        hipLaunchKernelGGL((attn_prefill_kernel<D, G, kTilePage>), dim3(blocks),
-                           dim3(64 * G * kLockstepRows<G>), lds, stream, p);
+        SR_LAUNCH("attn_prefill_kernel", (attn_prefill_kernel<D, G, kTilePage>), dim3(blocks),
+                  dim3(64 * G * kLockstepRows<G>), lds, stream, p);
     }
     return hipGetLastError();
 }
@@ -1846,12 +1846,12 @@ hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(attn_verify_kernel<D>, dim3(blocks), dim3(kVerifyThreads), lds, stream,
-                       vp);
+    SR_LAUNCH("attn_verify_kernel", attn_verify_kernel<D>, dim3(blocks), dim3(kVerifyThreads), lds,
+              stream, vp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attn_verify_combine_kernel<D>, dim3(combine_rows), dim3(64 * kCombineWaves),
-                       0, stream, vp);
+    SR_LAUNCH("attn_verify_combine_kernel", attn_verify_combine_kernel<D>, dim3(combine_rows),
+              dim3(64 * kCombineWaves), 0, stream, vp);
     return hipGetLastError();
 }
 

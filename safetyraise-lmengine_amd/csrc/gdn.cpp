@@ -200,6 +200,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
     safetyraise_kernel_context *context, const safetyraise_kernel_gdn_args *args) {
     if (context == nullptr) return kInvalid;
     Ctx *ctx = context;
+    TimerScope timer_scope(ctx);
     if (args == nullptr || args->struct_size < sizeof(safetyraise_kernel_gdn_args)) {
         return fail(ctx, kInvalid, "gdn args pointer or struct_size is invalid");
     }
@@ -242,6 +243,10 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
     }
     if (total > INT32_MAX / std::max<uint32_t>(pool->channels, 1)) {
         return fail(ctx, kOverflow, "too many rows");
+    }
+    if (!async) {
+        const int32_t pst = report_pending_async(ctx);
+        if (pst != kOk) return pst;
     }
     const size_t esz = bf16 ? 2 : 4;
     const size_t width = (size_t)pool->value_heads * pool->value_dim;

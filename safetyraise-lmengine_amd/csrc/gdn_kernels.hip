@@ -1079,8 +1079,8 @@ hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t blocks)
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(gdn_chunk_kernel<Conv>, dim3(blocks), dim3(kChunkThreads), sizeof(ChunkLds),
-                       stream, p);
+    SR_LAUNCH("gdn_chunk_kernel", gdn_chunk_kernel<Conv>, dim3(blocks), dim3(kChunkThreads),
+              sizeof(ChunkLds), stream, p);
     return hipGetLastError();
 }
 
@@ -1188,12 +1188,11 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
         if (head_kernel) {
             const dim3 grid(pool->value_heads, (uint32_t)n);
             if (p.conv_k == 4) {
-                hipLaunchKernelGGL((gdn_head_kernel<kHeadThreads, ConvK<4>>), grid, dim3(kHeadThreads),
-                                   0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
+                SR_LAUNCH("gdn_head_kernel", (gdn_head_kernel<kHeadThreads, ConvK<4>>), grid,
+                          dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
             } else {
-                hipLaunchKernelGGL((gdn_head_kernel<kHeadThreads, ConvChan>), grid,
-                                   dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word,
-                                   g.eps);
+                SR_LAUNCH("gdn_head_kernel", (gdn_head_kernel<kHeadThreads, ConvChan>), grid,
+                          dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
             }
         } else if (chunk_kernel) {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kVs);
@@ -1202,7 +1201,7 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
             if (e != hipSuccess) return e;
         } else {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kRows);
-            hipLaunchKernelGGL(gdn_delta_kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
+            SR_LAUNCH("gdn_delta_kernel", gdn_delta_kernel, dim3(blocks), dim3(kThreads), 0, stream, p);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -1220,7 +1219,8 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
     q.eps = g.eps;
     q.bf16_in = g.bf16_in ? 1 : 0;
     const uint32_t waves = total_rows * pool->value_heads;
-    hipLaunchKernelGGL(gdn_norm_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, q);
+    SR_LAUNCH("gdn_norm_gate_kernel", gdn_norm_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0,
+              stream, q);
     return hipGetLastError();
 }
 

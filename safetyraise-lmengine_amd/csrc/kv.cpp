@@ -165,6 +165,20 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_create(
     for (uint64_t i = 0; i < o.num_pages; ++i) {
         pool->free_pages[i] = (int32_t)(o.num_pages - 1 - i);  // page 0 handed out first
     }
+    if (o.page_order_seed != 0) {
+        // Fisher-Yates over the free list with a splitmix64 stream
+        uint64_t state = o.page_order_seed;
+        auto next = [&state]() {
+            uint64_t z = (state += 0x9E3779B97F4A7C15ull);
+            z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+            z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+            return z ^ (z >> 31);
+        };
+        for (uint64_t i = o.num_pages - 1; i > 0; --i) {
+            const uint64_t j = next() % (i + 1);
+            std::swap(pool->free_pages[i], pool->free_pages[j]);
+        }
+    }
     *out_pool = pool;
     return kOk;
 }

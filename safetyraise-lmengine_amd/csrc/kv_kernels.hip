@@ -142,7 +142,7 @@ hipError_t launch_page_table_set(hipStream_t s, int32_t *table, const uint32_t *
             u.idx[i] = idx[base + i];
             u.val[i] = val[base + i];
         }
-        hipLaunchKernelGGL(page_table_set_kernel, dim3(1), dim3(256), 0, s, u);
+        SR_LAUNCH("page_table_set_kernel", page_table_set_kernel, dim3(1), dim3(256), 0, s, u);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -168,7 +168,7 @@ hipError_t launch_kv_scatter(hipStream_t s, const safetyraise_kernel_kv_pool *po
     p.page_tokens = pool->page_tokens;
     p.bf16_in = bf16_in ? 1 : 0;
     const uint64_t work = tokens * pool->kv_heads * (pool->head_dim / 8);
-    hipLaunchKernelGGL(kv_scatter_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, p);
+    SR_LAUNCH("kv_scatter_kernel", kv_scatter_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
@@ -188,7 +188,7 @@ hipError_t launch_kv_gather(hipStream_t s, const safetyraise_kernel_kv_pool *poo
     p.head_dim = pool->head_dim;
     p.page_tokens = pool->page_tokens;
     const uint64_t work = tokens * pool->kv_heads * pool->head_dim;
-    hipLaunchKernelGGL(kv_gather_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, p);
+    SR_LAUNCH("kv_gather_kernel", kv_gather_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 

@@ -202,12 +202,15 @@ template <int DT, int kGroup>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
                uint32_t K, uint32_t splits) {
     const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile, splits);
-    if ((K & 7u) == 0) {
-        hipLaunchKernelGGL((linear_kernel<DT, true, kGroup>), grid, dim3(64 * kLinWaves), 0, stream, x, w, y,
-                           M, N, K);
+    // 16-byte loads need 16-byte aligned rows: K a multiple of 8 and x itself
+    // aligned (a device caller may pass a view that starts mid-vector; the
+    // weight is the plugin's own allocation)
+    if ((K & 7u) == 0 && ((uintptr_t)x & 15u) == 0) {
+        SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, kGroup>), grid, dim3(64 * kLinWaves), 0,
+                  stream, x, w, y, M, N, K);
     } else {
-        hipLaunchKernelGGL((linear_kernel<DT, false, kGroup>), grid, dim3(64 * kLinWaves), 0, stream, x, w,
-                           y, M, N, K);
+        SR_LAUNCH("linear_kernel", (linear_kernel<DT, false, kGroup>), grid, dim3(64 * kLinWaves), 0,
+                  stream, x, w, y, M, N, K);
     }
 }
 
@@ -244,7 +247,21 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
                          float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
                          int num_cus) {
     if (M == 0 || N == 0) return hipSuccess;
-    if (M > 65535u * kLinTile) return hipErrorInvalidValue;  // grid y limit
+    constexpr uint32_t kMaxRows = 65535u * kLinTile;  // grid y limit of one launch
+    if (M > kMaxRows) {
+        // equal blocks of rows, one launch each: every block has at least
+        // kMaxRows / 2 rows, so enough tiles that none splits K and the
+        // scratch (sized 0 for such M) is not used
+        const uint32_t nb = (M + kMaxRows - 1) / kMaxRows;
+        const uint32_t per = ((M + nb - 1) / nb + kLinTile - 1) / kLinTile * kLinTile;
+        for (uint32_t r0 = 0; r0 < M; r0 += per) {
+            const uint32_t m = std::min(per, M - r0);
+            const hipError_t e = launch_linear(stream, x + (size_t)r0 * K, w, dtype,
+                                               y + (size_t)r0 * N, m, N, K, nullptr, num_cus);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     const uint32_t splits = linear_splits(M, N, K, num_cus);
     if (splits > 1 && scratch == nullptr) return hipErrorInvalidValue;
     float *dst = splits > 1 ? scratch : y;
@@ -264,8 +281,8 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
     if (splits > 1) {
         // splits > 1 only when tiles < kLinWgPerCu * CUs, so M * N is small
         const uint32_t count = M * N;
-        hipLaunchKernelGGL(linear_split_sum_kernel, dim3((count + 255) / 256), dim3(256), 0, stream,
-                           scratch, y, count, splits);
+        SR_LAUNCH("linear_split_sum_kernel", linear_split_sum_kernel, dim3((count + 255) / 256),
+                  dim3(256), 0, stream, scratch, y, count, splits);
     }
     return hipGetLastError();
 }

@@ -64,6 +64,7 @@ int32_t ensure_buffer(Ctx *ctx, DeviceBuffer &buf, size_t bytes, bool zero) {
 int32_t take_error_word(Ctx *ctx, uint32_t *word) {
     SR_HIP(ctx, hipGetLastError());
     SR_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->async_pending = false;
     *word = 0;
     SR_HIP(ctx, hipMemcpy(word, ctx->d_error_word, sizeof *word, hipMemcpyDeviceToHost));
     if (*word != 0) {
@@ -82,19 +83,64 @@ int32_t error_word_status(Ctx *ctx, uint32_t word) {
         return fail(ctx, kInvalid, "KV append contains a non-finite value");
     }
     return fail(ctx, kInvalid,
-                "prefill attention met a K/V/q value outside the fp16 range of its MFMA "
-                "operands; repeat the call synchronously to recompute it on the f32 path");
+                "an asynchronous prefill or verify call met a K/V/q value outside the fp16 "
+                "range of its MFMA operands; truncate its sequences back (kv_truncate) and "
+                "repeat it synchronously to recompute it on the f32 path");
 }
 
 int32_t finish_call(Ctx *ctx, bool async) {
     SR_HIP(ctx, hipGetLastError());
     if (async) {
+        ctx->async_pending = true;
         return kOk;
     }
     uint32_t word = 0;
     int32_t st = take_error_word(ctx, &word);
     if (st != kOk) return st;
     return error_word_status(ctx, word);
+}
+
+int32_t report_pending_async(Ctx *ctx) {
+    if (!ctx->async_pending) return kOk;
+    uint32_t word = 0;
+    const int32_t st = take_error_word(ctx, &word);
+    if (st != kOk) return st;
+    return error_word_status(ctx, word);
+}
+
+namespace {
+thread_local KernelTimer *t_timer = nullptr;
+}
+
+TimerScope::TimerScope(Ctx *ctx) : prev_(t_timer) {
+    t_timer = (ctx != nullptr && ctx->timer.enabled) ? &ctx->timer : nullptr;
+}
+TimerScope::~TimerScope() { t_timer = prev_; }
+
+LaunchEvents timed_launch(const char *kernel) {
+    KernelTimer *t = t_timer;
+    if (t == nullptr) return {};
+    if (t->used == t->records.size()) {
+        KernelTimer::Record r{kernel, nullptr, nullptr};
+        if (hipEventCreate(&r.start) != hipSuccess) return {};
+        if (hipEventCreate(&r.stop) != hipSuccess) {
+            (void)hipEventDestroy(r.start);
+            return {};
+        }
+        t->records.push_back(r);
+    }
+    KernelTimer::Record &r = t->records[t->used++];
+    r.name = kernel;
+    return {r.start, r.stop};
+}
+
+static void destroy_timer_events(KernelTimer &t) {
+    for (auto &r : t.records) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    t.records.clear();
+    t.used = 0;
 }
 
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim) {
@@ -184,6 +230,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_destroy_context(
                             &context->linear_part}) {
         if (b->ptr != nullptr) (void)hipFree(b->ptr);
     }
+    destroy_timer_events(context->timer);
     if (context->d_error_word != nullptr) (void)hipFree(context->d_error_word);
     if (context->own_stream != nullptr) (void)hipStreamDestroy(context->own_stream);
     delete context;
@@ -307,6 +354,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear(
     if (context == nullptr) {
         return kInvalid;
     }
+    TimerScope timer_scope(context);
     uint64_t in_count = 0, out_count = 0;
     const int32_t st = check_linear(context, weight, input, input_rows, input_cols, output,
                                     output_rows, output_cols, &in_count, &out_count);
@@ -348,6 +396,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_linear_device(
     if (context == nullptr) {
         return kInvalid;
     }
+    TimerScope timer_scope(context);
     uint64_t in_count = 0, out_count = 0;
     const int32_t st = check_linear(context, weight, input, input_rows, input_cols, output,
                                     output_rows, output_cols, &in_count, &out_count);
@@ -386,6 +435,55 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_synchronize(
         return kInvalid;
     }
     return finish_call(context, false);
+}
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_timing_enable(
+    safetyraise_kernel_context *context, uint32_t enable) {
+    if (context == nullptr) {
+        return kInvalid;
+    }
+    // records of launches still queued must not be reused under them
+    SR_HIP(context, hipStreamSynchronize(context->stream));
+    context->timer.enabled = enable != 0;
+    context->timer.used = 0;
+    if (!context->timer.enabled) destroy_timer_events(context->timer);
+    return kOk;
+}
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_timing_read(
+    safetyraise_kernel_context *context, uint32_t index, const char **out_name,
+    uint64_t *out_launches, double *out_total_ms) {
+    if (context == nullptr) {
+        return kInvalid;
+    }
+    if (out_name == nullptr || out_launches == nullptr || out_total_ms == nullptr) {
+        return fail(context, kInvalid, "timing_read output pointer is NULL");
+    }
+    SR_HIP(context, hipStreamSynchronize(context->stream));
+    const KernelTimer &t = context->timer;
+    // distinct names in order of first launch
+    std::vector<const char *> names;
+    for (size_t i = 0; i < t.used; ++i) {
+        bool seen = false;
+        for (const char *n : names) seen = seen || std::strcmp(n, t.records[i].name) == 0;
+        if (!seen) names.push_back(t.records[i].name);
+    }
+    if (index >= names.size()) {
+        return fail(context, kInvalid, "timing_read index is past the last kernel name");
+    }
+    double total = 0.0;
+    uint64_t launches = 0;
+    for (size_t i = 0; i < t.used; ++i) {
+        if (std::strcmp(names[index], t.records[i].name) != 0) continue;
+        float ms = 0.0f;
+        SR_HIP(context, hipEventElapsedTime(&ms, t.records[i].start, t.records[i].stop));
+        total += ms;
+        ++launches;
+    }
+    *out_name = names[index];
+    *out_launches = launches;
+    *out_total_ms = total;
+    return kOk;
 }
 
 }  // extern "C"

@@ -1,11 +1,21 @@
 // Device helpers shared by the gfx950 kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 #include "sr_internal.hpp"
+
+// hipLaunchKernelGGL with the kernel timer's events for this launch (null
+// events, an ordinary launch, when timing is off).
+#define SR_LAUNCH(name, kernel, grid, block, lds, stream, ...)                              \
+    do {                                                                                    \
+        const ::sr::LaunchEvents _ev = ::sr::timed_launch(name);                            \
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, _ev.start, _ev.stop, 0,     \
+                              __VA_ARGS__);                                                 \
+    } while (0)
 
 namespace sr {
 

@@ -52,6 +52,28 @@ struct MetaPack {
     SeqMeta m[kMetaPerLaunch];
 };
 
+// Device durations of kernel launches, recorded on request
+// (safetyraise_kernel_timing_enable) with the start/stop events of
+// hipExtLaunchKernelGGL, i.e. the timestamps of the dispatch itself.  A
+// launcher asks timed_launch(name) for the events of one launch; they are
+// null (an ordinary launch) unless the calling thread is inside an entry
+// point of a context whose timing is on (TimerScope).
+struct KernelTimer {
+    struct Record {
+        const char *name;
+        hipEvent_t start;
+        hipEvent_t stop;
+    };
+    bool enabled = false;
+    std::vector<Record> records;  // events are reused after timing_reset
+    size_t used = 0;
+};
+struct LaunchEvents {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+LaunchEvents timed_launch(const char *kernel);
+
 // RoPE denominators theta^(2i/rotary_dim) for i < rotary_dim/2, computed on
 // the host with the C library powf in f32 exactly as math.rs:90-91 does.
 struct RopeTable {
@@ -67,6 +89,7 @@ struct safetyraise_kernel_context {
     hipStream_t stream = nullptr;
     std::string error;
     uint32_t *d_error_word = nullptr;  // sticky kernel-detected errors
+    bool async_pending = false;        // ASYNC work queued since the word was last read
     sr::DeviceBuffer staging;          // host-pointer mode device copies
     sr::DeviceBuffer partials;         // split-K partial (m, l, o) records
     sr::DeviceBuffer rope_scratch;     // prefill: per-row RoPE cos/sin
@@ -76,6 +99,7 @@ struct safetyraise_kernel_context {
     float rope_theta = 0.0f;
     uint32_t rope_dim = 0;
     sr::RopeTable rope{};
+    sr::KernelTimer timer;
 };
 
 // A linear weight [rows][cols] in its own dtype (F32, F16 or BF16), on the
@@ -142,9 +166,26 @@ int32_t hip_fail(Ctx *ctx, hipError_t err, const char *what);
         if (_e != hipSuccess) return ::sr::hip_fail((ctx), _e, #expr); \
     } while (0)
 
+// Makes ctx's kernel timer the calling thread's current one for the life of
+// the scope (every entry point that launches kernels opens one).
+class TimerScope {
+  public:
+    explicit TimerScope(Ctx *ctx);
+    ~TimerScope();
+    TimerScope(const TimerScope &) = delete;
+    TimerScope &operator=(const TimerScope &) = delete;
+
+  private:
+    KernelTimer *prev_;
+};
+
 bool checked_mul(uint64_t a, uint64_t b, uint64_t *out);
 int32_t ensure_buffer(Ctx *ctx, DeviceBuffer &buf, size_t bytes, bool zero);
 int32_t finish_call(Ctx *ctx, bool async);  // sync + sticky error check unless async
+// At the start of a synchronous call: waits for earlier ASYNC work, if any,
+// and reports the errors its kernels raised (as the header promises), so
+// that the error word the call reads at its end holds only its own bits.
+int32_t report_pending_async(Ctx *ctx);
 // Synchronises the context stream and returns the sticky error word, cleared.
 int32_t take_error_word(Ctx *ctx, uint32_t *word);
 // The status and message for a non-zero error word.
@@ -193,6 +234,20 @@ struct AttnLaunch {
     uint32_t tbl_n = 0;
 };
 constexpr uint32_t kInlineTable = 64;
+
+// Device scratch of one attention call: the split-K partial records (decode
+// and verify) and the prefill RoPE table.  Each function returns nullptr,
+// with the context's error text set, when it cannot provide `bytes`.  The
+// default grows context-owned buffers; the no-allocation entry point hands
+// out parts of a fixed region.
+struct AttnScratch {
+    float *(*partials)(void *user, size_t bytes);
+    void *(*rope)(void *user, size_t bytes);
+    void *user;
+};
+// safetyraise_kernel_attention_forward with the call's scratch from `scratch`.
+int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args *args,
+                               const AttnScratch &scratch);
 
 // Host inputs of the decode launch plan: the CU count and a way to get the
 // scratch for per-segment (max, sum, output) records (context-owned, grown

@@ -89,6 +89,8 @@ EXTENSION_SYMBOLS = (
     "safetyraise_kernel_gdn_write",
     "safetyraise_kernel_gdn_forward",
     "safetyraise_kernel_linear_device",
+    "safetyraise_kernel_timing_enable",
+    "safetyraise_kernel_timing_read",
 )
 
 
@@ -117,7 +119,7 @@ class KvOptions(C.Structure):
         ("num_pages", C.c_uint64),
         ("max_tokens", C.c_uint64),
         ("max_sequences", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("page_order_seed", C.c_uint32),
     ]
 
 
@@ -224,6 +226,9 @@ def _declare(lib: C.CDLL) -> None:
         "safetyraise_kernel_gdn_write": (i32, [vp, vp, u32, vp, vp]),
         "safetyraise_kernel_gdn_forward": (i32, [vp, C.POINTER(GdnArgs)]),
         "safetyraise_kernel_linear_device": (i32, [vp, vp, vp, u64, u64, vp, u64, u64]),
+        "safetyraise_kernel_timing_enable": (i32, [vp, u32]),
+        "safetyraise_kernel_timing_read": (i32, [vp, u32, C.POINTER(C.c_char_p), pu64,
+                                                 C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         if hasattr(lib, name):
@@ -384,6 +389,26 @@ class NativeBackend:
     def synchronize(self) -> None:
         self.check(self.lib.safetyraise_kernel_synchronize(self.context), "synchronizing")
 
+    def timing(self, enable: bool) -> None:
+        """Starts (and clears) or stops recording each kernel launch's device
+        duration (hipExtLaunchKernelGGL start/stop events)."""
+        self.check(self.lib.safetyraise_kernel_timing_enable(self.context, 1 if enable else 0),
+                   "switching kernel timing")
+
+    def kernel_times(self) -> dict:
+        """{kernel name: (launches, mean microseconds)} since timing(True)."""
+        out = {}
+        i = 0
+        while True:
+            name, n, ms = C.c_char_p(), C.c_uint64(), C.c_double()
+            st = self.lib.safetyraise_kernel_timing_read(self.context, i, C.byref(name),
+                                                         C.byref(n), C.byref(ms))
+            if st != STATUS_OK:
+                break
+            out[name.value.decode()] = (int(n.value), ms.value * 1e3 / max(int(n.value), 1))
+            i += 1
+        return out
+
 
 class Weight:
     """A prepared native weight (create_weight / destroy_weight)."""
@@ -402,11 +427,12 @@ class KvCache:
     """Paged bf16 KV pool; sequences are slots (PagedKvCache per slot)."""
 
     def __init__(self, backend: NativeBackend, kv_heads: int, head_dim: int, page_tokens: int,
-                 num_pages: int, max_tokens: int, max_sequences: int):
+                 num_pages: int, max_tokens: int, max_sequences: int, page_order_seed: int = 0):
+        """page_order_seed != 0 hands pages out in a seeded random order."""
         self.backend = backend
         self.kv_heads, self.head_dim, self.page_tokens = kv_heads, head_dim, page_tokens
         opts = KvOptions(C.sizeof(KvOptions), kv_heads, head_dim, page_tokens, num_pages,
-                         max_tokens, max_sequences, 0)
+                         max_tokens, max_sequences, page_order_seed)
         handle = C.c_void_p()
         backend.check(backend.lib.safetyraise_kernel_kv_create(backend.context, C.byref(opts),
                                                                C.byref(handle)), "kv_create")

@@ -142,6 +142,17 @@ def test_gdn_fork_is_an_independent_snapshot(pkg, backend, rng):
     fm, fh = pool.read(f)
     assert np.array_equal(fm, sm) and np.array_equal(fh, sh)
     assert out_f.shape == (3, 4 * 16)
+    # and matches the oracle run from the same snapshot
+    # (SequenceState::checkpoint then Gdn::forward, native.rs:720-742)
+    state = np.zeros((4, 16, 128), np.float32)
+    hist = np.zeros((L.C, L.K - 1), np.float32)
+    oracle_rows(L, x1, state, hist)
+    close(snap_m, state, what="snapshot state")
+    close(snap_h, hist, what="snapshot history")
+    exp = oracle_rows(L, x2, state, hist)
+    close(out_f, exp, what="fork replay output")
+    close(fm, state, what="fork state")
+    close(fh, hist, what="fork history")
     pool.destroy()
 
 

@@ -126,3 +126,36 @@ def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod, cols):
             C.c_void_p(dy.data_ptr()), 9, 130) == 1
     finally:
         prepared.destroy()
+
+
+def test_device_input_view_not_16_byte_aligned(backend, rng, torch_mod):
+    # a device input that starts one float into an allocation (a tensor view):
+    # the kernel must not read it with 16-byte vector loads
+    torch = torch_mod
+    x = rng.integers(-8, 9, size=(6, 264)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(40, 264)).astype(np.float32)
+    bits = weight_bits(w, BF16)
+    prepared = backend.create_weight(bits, BF16)
+    try:
+        flat = torch.zeros(6 * 264 + 1, device="cuda")
+        flat[1:] = torch.from_numpy(x.ravel()).cuda()
+        dx = flat[1:]
+        assert dx.data_ptr() % 16 == 4
+        dy = torch.zeros((6, 40), device="cuda")
+        backend.check(backend.lib.safetyraise_kernel_linear_device(
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), 6, 264,
+            C.c_void_p(dy.data_ptr()), 6, 40), "linear_device")
+        backend.synchronize()
+        assert np.array_equal(dy.cpu().numpy(), O.linear(x, bits, BF16))
+    finally:
+        prepared.destroy()
+
+
+def test_rows_beyond_one_launch_grid(backend, rng):
+    # more rows than one launch's grid covers (65535 row tiles of 16): the
+    # plugin splits the rows over launches (the reference takes any count)
+    rows = 65535 * 16 + 37
+    x = rng.integers(-4, 5, size=(rows, 8)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(3, 8)).astype(np.float32)
+    got = backend.linear(w, x, F32)
+    assert np.array_equal(got, O.linear(x, w, F32))
