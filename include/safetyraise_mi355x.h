@@ -213,6 +213,19 @@ typedef struct safetyraise_kernel_attention_args {
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
     safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args);
 
+/* safetyraise_kernel_attention_forward that allocates no device memory.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * Same arguments, kernels and results; DEVICE_POINTERS is required.  The
+ * call's scratch (split-K partial records, the per-row RoPE table) comes from
+ * a fixed 64 MiB region per GPU that the library holds from the first call on
+ * that GPU until the process ends.  A call that needs more fails with
+ * OUT_OF_MEMORY and its sequences keep their lengths.  Every call on one GPU
+ * shares that region, so calls that overlap on one GPU (other threads,
+ * contexts or streams) race; calls on one context are serial anyway. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward_noalloc(
+    safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args);
+
 /* ------------------------------------------------------------------------
  * Gated delta net — replaces RecurrentState (src/engine/state.rs:129-135)
  * and the per-row loop of Gdn::forward (src/model/native.rs:720-742).

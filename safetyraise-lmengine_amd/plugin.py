@@ -80,6 +80,7 @@ EXTENSION_SYMBOLS = (
     "safetyraise_kernel_kv_append",
     "safetyraise_kernel_kv_read",
     "safetyraise_kernel_attention_forward",
+    "safetyraise_kernel_attention_forward_noalloc",
     "safetyraise_kernel_gdn_create",
     "safetyraise_kernel_gdn_destroy",
     "safetyraise_kernel_gdn_open",
@@ -217,6 +218,7 @@ def _declare(lib: C.CDLL) -> None:
         "safetyraise_kernel_kv_append": (i32, [vp, vp, u32, vp, vp, u64, u32]),
         "safetyraise_kernel_kv_read": (i32, [vp, vp, u32, u64, u64, vp, vp]),
         "safetyraise_kernel_attention_forward": (i32, [vp, C.POINTER(AttentionArgs)]),
+        "safetyraise_kernel_attention_forward_noalloc": (i32, [vp, C.POINTER(AttentionArgs)]),
         "safetyraise_kernel_gdn_create": (i32, [vp, C.POINTER(GdnOptions), C.POINTER(vp)]),
         "safetyraise_kernel_gdn_destroy": (i32, [vp, vp]),
         "safetyraise_kernel_gdn_open": (i32, [vp, vp, pu32]),
