@@ -60,6 +60,7 @@ extern "C" {
 #define SAFETYRAISE_MI355X_NORM_OFFSET UINT32_C(0x10) /* weight + 1 (Qwen3.5 norms) */
 #define SAFETYRAISE_MI355X_GATED UINT32_C(0x20)      /* q rows are per-head [q, gate] */
 #define SAFETYRAISE_MI355X_MROPE_INTERLEAVED UINT32_C(0x40)
+#define SAFETYRAISE_MI355X_KEEP_ROWS UINT32_C(0x80) /* gdn_forward: allow gdn_rollback */
 
 /* Largest number of sequences one call may carry. */
 #define SAFETYRAISE_MI355X_MAX_BATCH 1024u
@@ -243,7 +244,10 @@ typedef struct safetyraise_kernel_gdn_options {
     uint32_t value_dim; /* 128 */
     uint32_t conv_kernel;
     uint32_t max_sequences;
-    uint32_t reserved;
+    /* 0, or the most rows per sequence a KEEP_ROWS call may carry (<= 64,
+     * value_dim 128): every sequence then has two state buffers, so that
+     * gdn_rollback can return it to the state after any row of such a call. */
+    uint32_t keep_rows;
 } safetyraise_kernel_gdn_options;
 
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_create(
@@ -270,6 +274,22 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_write(
     safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence,
     const float *matrix, const float *history);
 
+/* Commit of an MTP verify without re-running it.  Replaces the re-forward of
+ * the committed tokens in decode_round (src/engine/speculative.rs:242-247)
+ * for the recurrent layers; attention layers use kv_truncate.
+ * After a gdn_forward call with SAFETYRAISE_MI355X_KEEP_ROWS (on a pool
+ * created with keep_rows), returns the sequence's state and conv history to
+ * what they were after its first `rows` rows of that call (0: before the
+ * call; the call's own row count: unchanged).  The state is rebuilt from the
+ * pre-call buffer, which the KEEP_ROWS call only read, and the per-row decay,
+ * correction and key that call recorded: one state read and one write, with
+ * the element-wise operations of the forward.  Allowed until the sequence's
+ * next gdn_forward or gdn_write; repeated calls rebuild from the same
+ * pre-call state.  flags: SAFETYRAISE_MI355X_ASYNC or 0. */
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_rollback(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence,
+    uint32_t rows, uint32_t flags);
+
 /* For each sequence's rows, in order (src/model/native.rs:720-742):
  *   x    = silu(causal conv over qkv with the history), history shifted;
  *   o    = gated_delta_step(x, a, b, A_log, dt_bias) on the state;
@@ -277,7 +297,8 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_write(
  * Inputs: qkv [rows][C], z [rows][Hv*Dv], a and b [rows][Hv] (f32, or bf16
  * with INPUT_BF16); a_log, dt_bias [Hv], conv_weight [C][K], norm [Dv] f32.
  * Output: out [rows][Hv*Dv] f32.
- * Calls with at most 8 rows per sequence run the recurrence token by token
+ * KEEP_ROWS calls (see gdn_rollback), and calls with at most 8 rows per
+ * sequence, run the recurrence token by token
  * (one workgroup per sequence and value head, state in registers); longer
  * calls with value_dim 128 and a 16-byte aligned qkv run the chunked (WY)
  * form on f32 MFMA in chunks of 32 rows, which equals the token-serial

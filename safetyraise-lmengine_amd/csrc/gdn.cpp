@@ -22,6 +22,8 @@ namespace {
 
 using Pool = safetyraise_kernel_gdn_pool;
 
+constexpr uint32_t kMaxKeepRows = 64;
+
 int32_t check_seq(Ctx *ctx, Pool *pool, uint32_t seq) {
     if (pool == nullptr || seq >= pool->max_sequences || !pool->open[seq]) {
         return fail(ctx, kInvalid, "GDN sequence handle is not open");
@@ -29,7 +31,10 @@ int32_t check_seq(Ctx *ctx, Pool *pool, uint32_t seq) {
     return kOk;
 }
 
-float *state_ptr(Pool *pool, uint32_t seq) { return pool->d_state + (size_t)seq * pool->state_elems(); }
+// the sequence's current state buffer (which = 0) or its other one (1)
+float *state_ptr(Pool *pool, uint32_t seq, uint32_t which = 0) {
+    return pool->d_state + (size_t)pool->state_index(seq, which) * pool->state_elems();
+}
 
 float *history_ptr(Pool *pool, uint32_t seq, uint32_t parity) {
     return pool->d_history +
@@ -63,6 +68,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_create(
                     "GDN geometry is invalid (key_dim 128, value_dim a multiple of 16, "
                     "value_heads a multiple of key_heads, conv kernel 1..8)");
     }
+    if (o.keep_rows > kMaxKeepRows || (o.keep_rows > 0 && o.value_dim != 128)) {
+        return fail(context, kInvalid, "GDN keep_rows must be at most 64, with value_dim 128");
+    }
     Pool *pool = new (std::nothrow) Pool();
     if (pool == nullptr) return fail(context, kNoMemory, "gdn pool allocation failed");
     pool->key_heads = o.key_heads;
@@ -72,19 +80,28 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_create(
     pool->conv_kernel = o.conv_kernel;
     pool->max_sequences = o.max_sequences;
     pool->channels = 2 * o.key_heads * o.key_dim + o.value_heads * o.value_dim;
-    const size_t state_bytes = pool->state_elems() * o.max_sequences * sizeof(float);
+    pool->keep_rows = o.keep_rows;
+    const size_t state_bytes =
+        pool->state_elems() * pool->state_buffers() * o.max_sequences * sizeof(float);
     const size_t hist_bytes = std::max<size_t>(pool->history_elems(), 1) * 2 * o.max_sequences *
                               sizeof(float);
+    const size_t rec_bytes =
+        pool->record_elems() * o.keep_rows * (size_t)o.max_sequences * sizeof(float);
     hipError_t err = hipMalloc(&pool->d_state, state_bytes);
     if (err == hipSuccess) err = hipMalloc(&pool->d_history, hist_bytes);
+    if (err == hipSuccess && rec_bytes > 0) err = hipMalloc(&pool->d_records, rec_bytes);
     if (err != hipSuccess) {
         if (pool->d_state) (void)hipFree(pool->d_state);
         if (pool->d_history) (void)hipFree(pool->d_history);
+        if (pool->d_records) (void)hipFree(pool->d_records);
         delete pool;
         return hip_fail(context, err, "gdn pool allocation");
     }
     pool->open.assign(o.max_sequences, 0);
     pool->parity.assign(o.max_sequences, 0);
+    pool->state_par.assign(o.max_sequences, 0);
+    pool->kept.assign(o.max_sequences, Pool::kNoKept);
+    pool->kept_at.assign(o.max_sequences, 0);
     *out_pool = pool;
     return kOk;
 }
@@ -95,6 +112,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_destroy(
     SR_HIP(context, hipStreamSynchronize(context->stream));
     (void)hipFree(pool->d_state);
     (void)hipFree(pool->d_history);
+    if (pool->d_records != nullptr) (void)hipFree(pool->d_records);
     delete pool;
     return kOk;
 }
@@ -107,6 +125,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_open(
     if (pool == nullptr || out_sequence == nullptr) return fail(context, kInvalid, "NULL argument");
     for (uint32_t i = 0; i < pool->max_sequences; ++i) {
         if (!pool->open[i]) {
+            pool->state_par[i] = 0;
             SR_HIP(context, hipMemsetAsync(state_ptr(pool, i), 0,
                                            pool->state_elems() * sizeof(float), context->stream));
             if (pool->history_elems() > 0) {
@@ -116,6 +135,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_open(
             }
             pool->open[i] = 1;
             pool->parity[i] = 0;
+            pool->kept[i] = Pool::kNoKept;
             *out_sequence = i;
             return kOk;
         }
@@ -188,6 +208,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_write(
                                        pool->state_elems() * sizeof(float), hipMemcpyHostToDevice,
                                        context->stream));
     }
+    pool->kept[sequence] = Pool::kNoKept;
     if (history != nullptr && pool->history_elems() > 0) {
         SR_HIP(context, hipMemcpyAsync(history_ptr(pool, sequence, pool->parity[sequence]), history,
                                        pool->history_elems() * sizeof(float),
@@ -223,8 +244,11 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
         A.norm == nullptr || A.out == nullptr) {
         return fail(ctx, kInvalid, "GDN input or output pointer is NULL");
     }
-    std::vector<uint32_t> slots(A.num_seqs), rows(A.num_seqs), row0(A.num_seqs),
-        parity(A.num_seqs);
+    const bool keep = (A.flags & SAFETYRAISE_MI355X_KEEP_ROWS) != 0;
+    if (keep && pool->keep_rows == 0) {
+        return fail(ctx, kInvalid, "KEEP_ROWS needs a GDN pool created with keep_rows > 0");
+    }
+    std::vector<GdnSeq> seqs(A.num_seqs);
     uint64_t total = 0;
     for (uint32_t i = 0; i < A.num_seqs; ++i) {
         const int32_t st = check_seq(ctx, pool, A.seq_ids[i]);
@@ -235,10 +259,19 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
             }
         }
         if (A.seq_rows[i] == 0) return fail(ctx, kInvalid, "input is empty");
-        slots[i] = A.seq_ids[i];
-        rows[i] = A.seq_rows[i];
-        row0[i] = (uint32_t)total;
-        parity[i] = pool->parity[A.seq_ids[i]];
+        if (keep && A.seq_rows[i] > pool->keep_rows) {
+            return fail(ctx, kInvalid, "a KEEP_ROWS call has more rows than the pool's keep_rows");
+        }
+        const uint32_t id = A.seq_ids[i];
+        GdnSeq &q = seqs[i];
+        q.slot = id;
+        q.rows = A.seq_rows[i];
+        q.row0 = (uint32_t)total;
+        q.parity = pool->parity[id];
+        // KEEP_ROWS: read the current state buffer, write the other one (the
+        // pre-call state stays for gdn_rollback); otherwise update in place
+        q.state_in = pool->state_index(id, 0);
+        q.state_out = keep ? pool->state_index(id, 1) : q.state_in;
         total += A.seq_rows[i];
     }
     if (total > INT32_MAX / std::max<uint32_t>(pool->channels, 1)) {
@@ -306,13 +339,60 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
         g.norm = (const float *)(base + regions[7].off);
         g.out = (float *)(base + out_off);
     }
-    SR_HIP(ctx, launch_gdn(ctx->stream, g, slots.data(), rows.data(), row0.data(), parity.data(),
-                           (int)A.num_seqs, (uint32_t)total));
-    for (uint32_t i = 0; i < A.num_seqs; ++i) {
-        pool->parity[slots[i]] ^= 1u;
+    g.keep = keep;
+    g.records = pool->d_records;
+    g.rec_stride = (uint32_t)pool->record_elems();
+    g.keep_rows = pool->keep_rows;
+    SR_HIP(ctx, launch_gdn(ctx->stream, g, seqs.data(), (int)A.num_seqs, (uint32_t)total));
+    for (const GdnSeq &q : seqs) {
+        pool->parity[q.slot] ^= 1u;
+        if (keep) pool->state_par[q.slot] ^= 1u;
+        pool->kept[q.slot] = keep ? q.rows : Pool::kNoKept;
+        pool->kept_at[q.slot] = q.rows;
     }
     if (!device) {
         SR_HIP(ctx, hipMemcpyAsync(A.out, g.out, out_b, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    return finish_call(ctx, async);
+}
+
+SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_rollback(
+    safetyraise_kernel_context *context, safetyraise_kernel_gdn_pool *pool, uint32_t sequence,
+    uint32_t rows, uint32_t flags) {
+    if (context == nullptr) return kInvalid;
+    Ctx *ctx = context;
+    TimerScope timer_scope(ctx);
+    int32_t st = check_seq(ctx, pool, sequence);
+    if (st != kOk) return st;
+    const uint32_t kept = pool->kept[sequence];
+    if (kept == Pool::kNoKept) {
+        return fail(ctx, kInvalid,
+                    "gdn_rollback: the sequence's last call was not a KEEP_ROWS call");
+    }
+    if (rows > kept) {
+        return fail(ctx, kInvalid, "gdn_rollback: more rows than the KEEP_ROWS call had");
+    }
+    const bool async = (flags & SAFETYRAISE_MI355X_ASYNC) != 0;
+    if (!async) {
+        st = report_pending_async(ctx);
+        if (st != kOk) return st;
+    }
+    if (rows != pool->kept_at[sequence]) {
+        // rebuild the state and history after `rows` rows into the current
+        // buffers from the pre-call ones (which the KEEP_ROWS call only read)
+        GdnRollback r;
+        r.state_in = state_ptr(pool, sequence, 1);
+        r.state_out = state_ptr(pool, sequence, 0);
+        r.hist_in = history_ptr(pool, sequence, pool->parity[sequence] ^ 1u);
+        r.hist_out = history_ptr(pool, sequence, pool->parity[sequence]);
+        r.records = pool->d_records + (size_t)sequence * pool->keep_rows * pool->record_elems();
+        r.rec_stride = (uint32_t)pool->record_elems();
+        r.keep = rows;
+        r.value_heads = pool->value_heads;
+        r.channels = pool->channels;
+        r.conv_k = pool->conv_kernel;
+        SR_HIP(ctx, launch_gdn_rollback(ctx->stream, r));
+        pool->kept_at[sequence] = rows;
     }
     return finish_call(ctx, async);
 }

@@ -33,7 +33,9 @@ struct GdnMeta {
     uint32_t slot;
     uint32_t rows;
     uint32_t row0;
-    uint32_t parity;  // history buffer holding the current history
+    uint32_t parity;     // history buffer holding the current history
+    uint32_t state_in;   // state buffer read (index in units of one state)
+    uint32_t state_out;  // state buffer written (== state_in but for KEEP_ROWS calls)
 };
 
 struct GdnParams {
@@ -46,6 +48,13 @@ struct GdnParams {
     const float *dt_bias;
     const float *conv_w;     // [C][K]
     float *raw_out;          // [rows][Hv*Dv]
+    // KEEP_ROWS calls (gdn_head_kernel only): per (slot, row) the row's decay
+    // alpha [Hv], correction delta [Hv][Dv], normalised key k^ [Hv][Dk] and raw
+    // conv inputs x [C], from which gdn_rollback_kernel rebuilds the state and
+    // history after any row; nullptr otherwise
+    float *records;
+    uint32_t rec_stride;     // floats per (slot, row) record
+    uint32_t keep_rows;      // records per slot
     uint32_t key_heads, value_heads, value_dim, conv_k, channels, max_slots;
     int bf16_in;
     uint32_t nseq;
@@ -141,7 +150,7 @@ __global__ void __launch_bounds__(kThreads) gdn_delta_kernel(const GdnParams p) 
     };
 
     // state slice: row v_row, dims [8*l16, 8*l16+8)
-    float *srow = p.state + (((size_t)m.slot * p.value_heads + h) * p.value_dim + v_row) * kDk +
+    float *srow = p.state + (((size_t)m.state_in * p.value_heads + h) * p.value_dim + v_row) * kDk +
                   l16 * 8;
     float S[8];
     {
@@ -266,13 +275,15 @@ struct HeadArgs {
     const void *z;
     float *out;
     uint32_t *err_word;
+    float *records;
     float eps;
-    uint32_t key_heads, value_heads, conv_k, channels, max_slots;
+    uint32_t key_heads, value_heads, conv_k, channels, max_slots, rec_stride, keep_rows;
     int bf16_in;
     // forces every field into a register here, so all the reads are issued
     // together and waited for once
     __device__ __forceinline__ void pin() {
         state = pin_global(state);
+        records = pin_global(records);
         history = pin_global(history);
         qkv = pin_global(qkv);
         a = pin_global(a);
@@ -285,7 +296,8 @@ struct HeadArgs {
         out = pin_global(out);
         err_word = pin_global(err_word);
         asm volatile("" : "+s"(eps), "+s"(key_heads), "+s"(value_heads), "+s"(conv_k),
-                     "+s"(channels), "+s"(max_slots), "+s"(bf16_in));
+                     "+s"(channels), "+s"(max_slots), "+s"(rec_stride), "+s"(keep_rows),
+                     "+s"(bf16_in));
     }
 };
 constexpr int kHeadCh = 2 * kDk + kHeadDv;  // q, k and v channels of one head
@@ -314,8 +326,8 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // to locate it, so it is read in the same batch
     const GdnMeta m = p.meta[blockIdx.y];
     HeadArgs a{p.state, p.history, p.qkv, p.a, p.b, p.a_log, p.dt_bias, p.conv_w, norm, z, out,
-               err_word, eps, p.key_heads, p.value_heads, p.conv_k, p.channels, p.max_slots,
-               p.bf16_in};
+               err_word, p.records, eps, p.key_heads, p.value_heads, p.conv_k, p.channels,
+               p.max_slots, p.rec_stride, p.keep_rows, p.bf16_in};
     a.pin();
     const bool bf16_in = a.bf16_in != 0;
 
@@ -364,7 +376,12 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     // then covers 256 contiguous bytes of a row; requested after
     // the (branchy) conv loads so that nothing waits for them before the
     // delta step itself
-    float *sbase = a.state + ((size_t)m.slot * a.value_heads + h) * kHeadDv * kDk + l16 * 4;
+    float *sbase = a.state + ((size_t)m.state_in * a.value_heads + h) * kHeadDv * kDk + l16 * 4;
+    float *obase = a.state + ((size_t)m.state_out * a.value_heads + h) * kHeadDv * kDk + l16 * 4;
+    // KEEP_ROWS: this head's part of each row's record (alpha, delta, k^, x)
+    const bool keep = a.records != nullptr;  // uniform
+    const uint32_t hv_dv = a.value_heads * kHeadDv;
+    const bool owns_qk = (h % groups == 0);
     // the state is read once and written once per call: nontemporal
     // accesses (streaming reads measured ~8 % faster than ordinary loads)
     typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
@@ -385,15 +402,25 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
 
     for (uint32_t r = 0; r < m.rows; ++r) {
         const size_t row = (size_t)m.row0 + r;
+        float *rec = keep ? a.records + ((size_t)m.slot * a.keep_rows + r) * a.rec_stride : nullptr;
         // A. causal conv + silu (math.rs:175-185), history in registers
         if (one) conv_s[tid] = cv0.step(x0, a.conv_k);
         if constexpr (kTwo) {
             if (two) conv_s[tid + NTH] = cv1.step(x1, a.conv_k);
         }
+        if (keep) {
+            // the row's raw conv inputs (q/k channels by the key group's first head)
+            float *rx = rec + a.value_heads + 2 * hv_dv;
+            if (one && (tid >= 2 * kDk || owns_qk)) rx[ch0] = x0;
+            if constexpr (kTwo) {
+                if (two && (tid + NTH >= 2 * kDk || owns_qk)) rx[ch1] = x1;
+            }
+        }
         if (tid == 0) {
             // math.rs:220-221
             ab_s[0] = expf(-a_log_e * softplus_ref(av + dt));
             ab_s[1] = ref_sigmoid(bv);
+            if (keep) rec[h] = ab_s[0];
         }
         const float zc0 = z0, zc1 = z1;
         load_row(m.row0 + min(r + 1, m.rows - 1));  // next row's inputs (unconditional)
@@ -417,6 +444,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
             const int dim = (j < 4) ? 4 * l16 + j : kDk / 2 + 4 * l16 + (j - 4);
             kh8[j] = conv_s[kDk + dim] * ki;
             qh8[j] = conv_s[dim] * qi;
+            if (keep && group == 0) rec[a.value_heads + hv_dv + h * kDk + dim] = kh8[j];
         }
 #pragma unroll
         for (int i = 0; i < RPG; ++i) {
@@ -429,6 +457,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
             }
             pred = sum16(pred);
             const float corr = beta * (conv_s[2 * kDk + v] - pred);
+            if (keep && l16 == 0) rec[a.value_heads + h * kHeadDv + v] = corr;
             float rd = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -440,7 +469,7 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
             if (r + 1 == m.rows) {
                 // final values of this slice: written now, so that the state
                 // writes stream out while later slices are still arriving
-                float *dst = sbase + (size_t)v * kDk;
+                float *dst = obase + (size_t)v * kDk;
                 __builtin_nontemporal_store(nt_f32x4{S[i][0], S[i][1], S[i][2], S[i][3]},
                                             (nt_f32x4 *)dst);
                 __builtin_nontemporal_store(nt_f32x4{S[i][4], S[i][5], S[i][6], S[i][7]},
@@ -463,10 +492,82 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
 
     // next history: v channels here; q/k channels by the first value head of
     // the key group (the others compute the same values)
-    const bool owns_qk = (h % groups == 0);
     if (one && (tid >= 2 * kDk || owns_qk)) cv0.store(a.history + (hist_next + ch0) * K1, a.conv_k);
     if constexpr (kTwo) {
         if (two && (tid + NTH >= 2 * kDk || owns_qk)) cv1.store(a.history + (hist_next + ch1) * K1, a.conv_k);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gdn_rollback_kernel: one sequence's state and conv history as they were
+// after row `keep` of its last KEEP_ROWS call, rebuilt from the state before
+// that call (the other state buffer, which the call only read) and the call's
+// records.  Per row the state update is S = alpha S + delta k^T, applied
+// element by element with the same operations gdn_head_kernel applies (a
+// product, then a multiply-add), so the rebuilt state is the one the forward
+// held after that row; the history is the last K-1 of (the history before
+// the call, x_0 .. x_{keep-1}).  Blocks 0..Hv-1 rebuild one value head's
+// state each, the others 256 conv channels each.
+// ---------------------------------------------------------------------------
+struct RollbackParams {
+    const float *state_in;  // [Hv][Dv][Dk] before the call
+    float *state_out;       // [Hv][Dv][Dk] the sequence's current buffer
+    const float *hist_in;   // [C][K-1] before the call
+    float *hist_out;        // [C][K-1] the current history buffer
+    const float *records;   // the sequence's records, rows 0 .. keep-1
+    uint32_t rec_stride, keep, value_heads, channels, conv_k;
+};
+
+__global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams p) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t hv_dv = p.value_heads * kHeadDv;
+    if (blockIdx.x < p.value_heads) {
+        const uint32_t h = blockIdx.x;
+        const uint32_t l16 = tid & 15, g = tid >> 4;  // rows g + 16 i, dims 8 l16 .. + 8
+        const float *src = p.state_in + (size_t)h * kHeadDv * kDk + 8 * l16;
+        float *dst = p.state_out + (size_t)h * kHeadDv * kDk + 8 * l16;
+        float S[8][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float *s = src + (size_t)(g + 16 * i) * kDk;
+            const float4 x0 = *(const float4 *)s, x1 = *(const float4 *)(s + 4);
+            S[i][0] = x0.x; S[i][1] = x0.y; S[i][2] = x0.z; S[i][3] = x0.w;
+            S[i][4] = x1.x; S[i][5] = x1.y; S[i][6] = x1.z; S[i][7] = x1.w;
+        }
+        for (uint32_t r = 0; r < p.keep; ++r) {
+            const float *rec = p.records + (size_t)r * p.rec_stride;
+            const float alpha = rec[h];
+            float kh[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) kh[j] = rec[p.value_heads + hv_dv + h * kDk + 8 * l16 + j];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float corr = rec[p.value_heads + h * kHeadDv + g + 16 * i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    S[i][j] *= alpha;
+                    S[i][j] += corr * kh[j];
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float *d = dst + (size_t)(g + 16 * i) * kDk;
+            *(float4 *)d = make_float4(S[i][0], S[i][1], S[i][2], S[i][3]);
+            *(float4 *)(d + 4) = make_float4(S[i][4], S[i][5], S[i][6], S[i][7]);
+        }
+        return;
+    }
+    const uint32_t c = (blockIdx.x - p.value_heads) * 256 + tid;
+    const uint32_t K1 = p.conv_k - 1;
+    if (c >= p.channels || K1 == 0) return;
+    // position t of (history before the call, x_0, x_1, ...): the last K-1
+    // positions up to row keep - 1 are t = keep .. keep + K1 - 1
+    for (uint32_t i = 0; i < K1; ++i) {
+        const uint32_t t = p.keep + i;
+        p.hist_out[(size_t)c * K1 + i] =
+            t < K1 ? p.hist_in[(size_t)c * K1 + t]
+                   : p.records[(size_t)(t - K1) * p.rec_stride + p.value_heads + 2 * hv_dv + c];
     }
 }
 
@@ -665,7 +766,7 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParam
     // state slice -> LDS (16 floats per thread, as 4 spans of 4 that are 32
     // floats apart: each 16-byte access instruction covers 128 contiguous
     // bytes of a row)
-    float *state = p.state + (((size_t)m.slot * p.value_heads + h) * p.value_dim + vq * kVs) * kDk;
+    float *state = p.state + (((size_t)m.state_in * p.value_heads + h) * p.value_dim + vq * kVs) * kDk;
     {
         const int v = tid >> 3, d0 = (tid & 7) * 4;
 #pragma unroll
@@ -1148,16 +1249,18 @@ __global__ void __launch_bounds__(256) gdn_norm_gate_kernel(const NormParams p) 
 
 }  // namespace
 
-hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,
-                      const uint32_t *rows, const uint32_t *row0, const uint32_t *parity, int nseq,
+hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs, int nseq,
                       uint32_t total_rows) {
     const auto *pool = g.pool;
     // decode-sized calls (at most kHeadKernelRows rows per sequence) run one
     // workgroup per (sequence, value head) with the norm and gate fused;
-    // longer chunks split each head's state rows over workgroups
+    // longer chunks split each head's state rows over workgroups.  KEEP_ROWS
+    // calls (records of every row) always take the token-serial head kernel.
     uint32_t max_rows = 0;
-    for (int i = 0; i < nseq; ++i) max_rows = rows[i] > max_rows ? rows[i] : max_rows;
-    const bool head_kernel = pool->value_dim == kHeadDv && max_rows <= kHeadKernelRows;
+    for (int i = 0; i < nseq; ++i) max_rows = seqs[i].rows > max_rows ? seqs[i].rows : max_rows;
+    if (g.keep && pool->value_dim != kHeadDv) return hipErrorInvalidValue;
+    const bool head_kernel =
+        pool->value_dim == kHeadDv && (max_rows <= kHeadKernelRows || g.keep);
     // longer calls with Dv = 128 take the chunked MFMA form (which reads the
     // qkv rows in 16-byte segments)
     const bool chunk_kernel = pool->value_dim == kHeadDv && !head_kernel &&
@@ -1174,6 +1277,9 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
         p.dt_bias = g.dt_bias;
         p.conv_w = g.conv_w;
         p.raw_out = g.raw;
+        p.records = g.keep ? g.records : nullptr;
+        p.rec_stride = g.rec_stride;
+        p.keep_rows = g.keep_rows;
         p.key_heads = pool->key_heads;
         p.value_heads = pool->value_heads;
         p.value_dim = pool->value_dim;
@@ -1183,7 +1289,8 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
         p.bf16_in = g.bf16_in ? 1 : 0;
         p.nseq = (uint32_t)n;
         for (int i = 0; i < n; ++i) {
-            p.meta[i] = GdnMeta{slots[base + i], rows[base + i], row0[base + i], parity[base + i]};
+            const GdnSeq &q = seqs[base + i];
+            p.meta[i] = GdnMeta{q.slot, q.rows, q.row0, q.parity, q.state_in, q.state_out};
         }
         if (head_kernel) {
             const dim3 grid(pool->value_heads, (uint32_t)n);
@@ -1221,6 +1328,23 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *sl
     const uint32_t waves = total_rows * pool->value_heads;
     SR_LAUNCH("gdn_norm_gate_kernel", gdn_norm_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0,
               stream, q);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r) {
+    RollbackParams p;
+    p.state_in = r.state_in;
+    p.state_out = r.state_out;
+    p.hist_in = r.hist_in;
+    p.hist_out = r.hist_out;
+    p.records = r.records;
+    p.rec_stride = r.rec_stride;
+    p.keep = r.keep;
+    p.value_heads = r.value_heads;
+    p.channels = r.channels;
+    p.conv_k = r.conv_k;
+    const uint32_t blocks = r.value_heads + (r.channels + 255) / 256;
+    SR_LAUNCH("gdn_rollback_kernel", gdn_rollback_kernel, dim3(blocks), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

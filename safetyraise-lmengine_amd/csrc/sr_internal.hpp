@@ -146,12 +146,29 @@ struct safetyraise_kernel_gdn_pool {
     uint32_t conv_kernel = 0;
     uint32_t max_sequences = 0;
     uint32_t channels = 0;
-    float *d_state = nullptr;    // [max_sequences][Hv][Dv][Dk]
-    float *d_history = nullptr;  // [max_sequences][C][K-1], oldest first
+    // rows a KEEP_ROWS call may carry per sequence (0: no rollback); with it
+    // every sequence has two state buffers and a record per row
+    uint32_t keep_rows = 0;
+    float *d_state = nullptr;    // [max_sequences][1 or 2][Hv][Dv][Dk]
+    float *d_history = nullptr;  // [2][max_sequences][C][K-1], oldest first
+    float *d_records = nullptr;  // [max_sequences][keep_rows][record_elems()]
     std::vector<uint8_t> open;
-    std::vector<uint32_t> parity;  // which history buffer is current
+    std::vector<uint32_t> parity;     // which history buffer is current
+    std::vector<uint32_t> state_par;  // which state buffer is current (keep_rows > 0)
+    std::vector<uint32_t> kept;       // rows of the last KEEP_ROWS call, kNoKept if none since
+    std::vector<uint32_t> kept_at;    // row of that call the current buffers hold
+    static constexpr uint32_t kNoKept = 0xffffffffu;
     size_t state_elems() const { return (size_t)value_heads * value_dim * key_dim; }
     size_t history_elems() const { return (size_t)channels * (conv_kernel - 1); }
+    uint32_t state_buffers() const { return keep_rows > 0 ? 2u : 1u; }
+    // state buffer index of a sequence's current (which = 0) or other (1) buffer
+    uint32_t state_index(uint32_t seq, uint32_t which) const {
+        return seq * state_buffers() + (keep_rows > 0 ? (state_par[seq] ^ which) : 0u);
+    }
+    // alpha [Hv], delta [Hv][Dv], k^ [Hv][Dk], raw conv inputs [C]
+    size_t record_elems() const {
+        return (size_t)value_heads * (1 + value_dim + key_dim) + channels;
+    }
 };
 
 namespace sr {
@@ -289,7 +306,30 @@ struct GdnLaunch {
     uint32_t *err_word;
     float eps;
     bool bf16_in;
+    // KEEP_ROWS: every row's record goes to records[slot][row] (rec_stride
+    // floats each, keep_rows per slot)
+    bool keep = false;
+    float *records = nullptr;
+    uint32_t rec_stride = 0, keep_rows = 0;
 };
+
+// One sequence of a GDN launch: pool slot, its rows in the call, the
+// current history buffer, and the state buffers read and written (indices in
+// units of one sequence's state; equal except for KEEP_ROWS calls).
+struct GdnSeq {
+    uint32_t slot, rows, row0, parity, state_in, state_out;
+};
+
+// gdn_rollback_kernel's inputs for one sequence.
+struct GdnRollback {
+    const float *state_in;
+    float *state_out;
+    const float *hist_in;
+    float *hist_out;
+    const float *records;
+    uint32_t rec_stride, keep, value_heads, channels, conv_k;
+};
+hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r);
 
 // y[M][N] = x[M][K] . W[N][K]^T on f32 MFMA, W of dtype F32/F16/BF16
 // (linear_kernels.hip).  scratch holds linear_scratch_bytes(...) bytes of
@@ -300,8 +340,7 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
                          int num_cus);
 
 // Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
-hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const uint32_t *slots,
-                      const uint32_t *rows, const uint32_t *row0, const uint32_t *parity, int nseq,
+hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs, int nseq,
                       uint32_t total_rows);
 uint32_t gdn_key_dim();
 uint32_t gdn_row_block();

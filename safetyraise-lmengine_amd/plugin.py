@@ -54,6 +54,7 @@ QK_NORM = 0x8
 NORM_OFFSET = 0x10
 GATED = 0x20
 MROPE_INTERLEAVED = 0x40
+KEEP_ROWS = 0x80
 
 V1_SYMBOLS = (
     "safetyraise_kernel_abi_version",
@@ -89,6 +90,7 @@ EXTENSION_SYMBOLS = (
     "safetyraise_kernel_gdn_read",
     "safetyraise_kernel_gdn_write",
     "safetyraise_kernel_gdn_forward",
+    "safetyraise_kernel_gdn_rollback",
     "safetyraise_kernel_linear_device",
     "safetyraise_kernel_timing_enable",
     "safetyraise_kernel_timing_read",
@@ -158,7 +160,7 @@ class GdnOptions(C.Structure):
         ("value_dim", C.c_uint32),
         ("conv_kernel", C.c_uint32),
         ("max_sequences", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("keep_rows", C.c_uint32),
     ]
 
 
@@ -227,6 +229,7 @@ def _declare(lib: C.CDLL) -> None:
         "safetyraise_kernel_gdn_read": (i32, [vp, vp, u32, vp, vp]),
         "safetyraise_kernel_gdn_write": (i32, [vp, vp, u32, vp, vp]),
         "safetyraise_kernel_gdn_forward": (i32, [vp, C.POINTER(GdnArgs)]),
+        "safetyraise_kernel_gdn_rollback": (i32, [vp, vp, u32, u32, u32]),
         "safetyraise_kernel_linear_device": (i32, [vp, vp, vp, u64, u64, vp, u64, u64]),
         "safetyraise_kernel_timing_enable": (i32, [vp, u32]),
         "safetyraise_kernel_timing_read": (i32, [vp, u32, C.POINTER(C.c_char_p), pu64,
@@ -540,13 +543,14 @@ class GdnState:
     """Per-sequence GDN recurrent state pool (RecurrentState per slot)."""
 
     def __init__(self, backend: NativeBackend, key_heads: int, value_heads: int, key_dim: int,
-                 value_dim: int, conv_kernel: int, max_sequences: int):
+                 value_dim: int, conv_kernel: int, max_sequences: int, keep_rows: int = 0):
+        """keep_rows > 0: KEEP_ROWS calls of up to that many rows can be rolled back."""
         self.backend = backend
         self.key_heads, self.value_heads = key_heads, value_heads
         self.key_dim, self.value_dim, self.conv_kernel = key_dim, value_dim, conv_kernel
         self.channels = 2 * key_heads * key_dim + value_heads * value_dim
         opts = GdnOptions(C.sizeof(GdnOptions), key_heads, value_heads, key_dim, value_dim,
-                          conv_kernel, max_sequences, 0)
+                          conv_kernel, max_sequences, keep_rows)
         handle = C.c_void_p()
         backend.check(backend.lib.safetyraise_kernel_gdn_create(backend.context, C.byref(opts),
                                                                 C.byref(handle)), "gdn_create")
@@ -580,6 +584,10 @@ class GdnState:
         h = np.ascontiguousarray(history, dtype=np.float32)
         self._call("write", seq, m.ctypes.data, h.ctypes.data)
 
+    def rollback(self, seq: int, rows: int, asynchronous: bool = False) -> None:
+        """State and history after the first `rows` rows of the last KEEP_ROWS call."""
+        self._call("rollback", seq, rows, ASYNC if asynchronous else 0)
+
     def destroy(self) -> None:
         if self.handle is not None and self.handle.value:
             self.backend.lib.safetyraise_kernel_gdn_destroy(self.backend.context, self.handle)
@@ -588,9 +596,10 @@ class GdnState:
 
 def gdn_forward(backend: NativeBackend, state: GdnState, seq_ids: Sequence[int],
                 seq_rows: Sequence[int], qkv, z, a, b, a_log, dt_bias, conv_weight, norm, out,
-                *, eps: float = 1e-6, asynchronous: bool = False) -> None:
-    """Gdn::forward row loop (src/model/native.rs:720-742) for a batch."""
-    flags = 0
+                *, eps: float = 1e-6, asynchronous: bool = False, keep_rows: bool = False) -> None:
+    """Gdn::forward row loop (src/model/native.rs:720-742) for a batch; keep_rows
+    records every row so that GdnState.rollback can return to any of them."""
+    flags = KEEP_ROWS if keep_rows else 0
     if _is_device(qkv):
         flags |= DEVICE_POINTERS
         if asynchronous:
