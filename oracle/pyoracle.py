@@ -77,6 +77,8 @@ def lib() -> C.CDLL:
                                          opt_f32, f, f, sz, vp, i, vp, _f32p, i]
         L.sro_linear.restype = i
         L.sro_linear.argtypes = [_f32p, sz, sz, vp, C.c_uint32, sz, _f32p]
+        L.sro_silu_mul.restype = None
+        L.sro_silu_mul.argtypes = [_f32p, _f32p, sz, _f32p]
         L.sro_gdn_rows.restype = i
         L.sro_gdn_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, _f32p, _f32p, _f32p, sz, _f32p,
                                    f, sz, sz, sz, sz, _f32p, _f32p, _f32p]
@@ -246,6 +248,15 @@ def gdn_rows(qkv, z, a, b, a_log, dt_bias, conv_weight, kernel: int, norm, eps: 
                            f32(a_log), f32(dt_bias), f32(conv_weight).ravel(), kernel, f32(norm),
                            eps, key_heads, value_heads, key_dim, value_dim,
                            history.reshape(-1), state.reshape(-1), out.ravel()), "gdn_rows")
+    return out
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    """silu(gate) * up element-wise (the MLP of Block::forward, native.rs:550-552)."""
+    g, u = f32(gate), f32(up)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().sro_silu_mul(g.ravel(), u.ravel(), g.size, out.ravel())
     return out
 
 

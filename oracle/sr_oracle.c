@@ -577,6 +577,12 @@ static float sro_weight_value(const void *weight, uint32_t dtype, size_t index) 
     return f;
 }
 
+void sro_silu_mul(const float *gate, const float *up, size_t n, float *out) {
+    for (size_t i = 0; i < n; ++i) {
+        out[i] = sro_silu(gate[i]) * up[i]; /* native.rs:551 */
+    }
+}
+
 int sro_linear(const float *input, size_t rows, size_t cols, const void *weight,
                uint32_t dtype, size_t out_features, float *output) {
     if (dtype < 1u || dtype > 3u) {

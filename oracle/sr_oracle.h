@@ -96,6 +96,10 @@ int sro_gdn_rows(const float *qkv, const float *z, const float *a, const float *
  * sum over c, in order, of input[r][c] * weight[o][c] in f32, with the weight
  * widened exactly from its dtype (1 = f32, 2 = f16 as :47-78, 3 = bf16 by
  * shift).  Returns 1 for a non-finite input (:221-226) or an unknown dtype. */
+/* src/model/native.rs:550-552 (Block::forward, the MLP): out[i] =
+ * silu(gate[i]) * up[i], with math.rs:20-22's silu. */
+void sro_silu_mul(const float *gate, const float *up, size_t n, float *out);
+
 int sro_linear(const float *input, size_t rows, size_t cols, const void *weight,
                uint32_t dtype, size_t out_features, float *output);
 
