@@ -517,8 +517,21 @@ __device__ void decode_segment(const DecodeParams &p, DecodeShared<D, G> &sh, in
             load_chunk(ka, va, s0);
             load_chunk(kb, vb, s0 + 1);
         }
-        auto run = [&](const Frag<DPL>(&kb)[4], const Frag<DPL>(&vb)[4], uint32_t c) {
+        auto run = [&](const Frag<DPL>(&kb)[4], Frag<DPL>(&vb)[4], uint32_t c) {
             const bool masked = c * kChunk < t0 || c * kChunk + kChunk > t1;
+            if (masked) {
+                // a masked token's probability is 0, but its V slot may hold
+                // any bits (never written, or past a truncation) and 0 * NaN
+                // is NaN: its V words are replaced by zeros
+#pragma unroll
+                for (int ps = 0; ps < 4; ++ps) {
+                    const uint32_t tok = c * kChunk + ps * 16 + group;
+                    if (tok < t0 || tok >= t1) {
+#pragma unroll
+                        for (int w = 0; w < DPL / 2; ++w) vb[ps].w[w] = 0u;
+                    }
+                }
+            }
             if constexpr (kTransposed) {
                 process_t(kb, vb, c, masked);
             } else {

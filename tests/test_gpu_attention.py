@@ -217,6 +217,28 @@ def test_kv_append_rejects_non_finite_and_keeps_length(pkg, backend):
     pool.destroy()
 
 
+@pytest.mark.parametrize("heads,page", [(16, 16), (16, 64), (32, 16), (32, 64)])
+@pytest.mark.parametrize("rows", [1, 3, 20])
+def test_non_finite_bits_past_the_length_are_never_read(pkg, backend, rng, heads, page, rows):
+    # A rejected append leaves its rows in the slots past the length (the
+    # length stays, as the reference's does).  The kernels load whole chunks
+    # and tiles, so the slots past the last token are read; their scores are
+    # masked and their V must not turn the output into NaN (0 * NaN).  G = 2
+    # and G = 4; decode (1 row), verify (3) and prefill (20); pages of 16 and
+    # 64 tokens.
+    pool = new_pool(pkg, backend, 8, 128, page_tokens=page, max_tokens=512, seqs=2)
+    gq = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    gk = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    case = Case(rng, pool, heads, 8, 128, ctx=37, rows=rows)
+    nan = np.full((80, 8 * 128), np.nan, np.float32)
+    with pytest.raises(pkg.PluginError):
+        pool.append(case.seq, nan, nan)
+    assert pool.len(case.seq) == 37
+    out = run_case(pkg, backend, pool, [case], rotary=128, gq=gq, gk=gk)
+    assert np.isfinite(out).all()
+    pool.destroy()
+
+
 # ---------------------------------------------------------------------------
 # attention parity
 # ---------------------------------------------------------------------------
