@@ -875,30 +875,33 @@ __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_
     }
 }
 
-// S^T = K Q^T for the 64 keys of a tile (two 32-key accumulators, operands
-// read two k-steps ahead of their MFMA).
+// S^T = K Q^T + c0 for the 64 keys of a tile (two 32-key accumulators that
+// start from c0, operands read two k-steps ahead of their MFMA).
 template <int D>
 __device__ __forceinline__ void s_tile(const unsigned char *kt, const f16x8 (&qop)[D / 16], int h,
-                                       int col, f32x16 (&sacc)[2]) {
+                                       int col, f32x16 (&sacc)[2], const f32x16 &c0) {
     constexpr int NS = D / 16;
     auto k_frag = [&](int u, int st) -> f16x8 {
         const int key = 32 * u + col;
         return *(const f16x8 *)(kt + key * (D * 2) + (((2 * st + h) ^ k_swz<D>(key)) * 16));
     };
-    sacc[0] = f32x16{};
-    sacc[1] = f32x16{};
     f16x8 ka[2][2] = {{k_frag(0, 0), k_frag(1, 0)}, {k_frag(0, 1), k_frag(1, 1)}};
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int st = 0; st < NS; ++st) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 1][u], qop[st], sacc[u], 0, 0,
-                                                             0);
+            sacc[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka[st & 1][u], qop[st],
+                                                             st == 0 ? c0 : sacc[u], 0, 0, 0);
             if (st + 2 < NS) ka[st & 1][u] = k_frag(u, st + 2);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+template <int D>
+__device__ __forceinline__ void s_tile(const unsigned char *kt, const f16x8 (&qop)[D / 16], int h,
+                                       int col, f32x16 (&sacc)[2]) {
+    s_tile<D>(kt, qop, h, col, sacc, f32x16{});
 }
 
 // O^T += V^T P^T (operands read one k-step ahead of their MFMA).
@@ -1039,6 +1042,84 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&sacc)[2], uint32_t key0, b
 #pragma unroll
             for (int i = 0; i < 16; ++i) oacc[tt][i] *= alpha;
     }
+}
+
+// A lane's partial row sum of one tile's fp16 probabilities at or below this
+// bound proves each of them finite (every p <= the sum < fp16's largest).
+constexpr float kPSumMax = 32768.0f;
+
+// Online softmax of one tile against a reference maximum m that moves rarely
+// (math.rs:133-148 in the log2 domain).  The S MFMAs start from -m (negm),
+// so sacc holds s - m and p = 2^(s - m) takes one exp per score; softmax is
+// shift-invariant, so o = sum p v / sum p does not depend on m as long as
+// every p is finite in fp16 and the largest is not far below 1.  m is the
+// row maximum of the block's first tile (it holds key 0, which every row
+// sees); it is raised, with l and O rescaled and the tile's p recomputed,
+// only when a lane's partial sum exceeds kPSumMax: one wave-uniform branch,
+// taken on the first tile and then only for a score ~15 (log2) above m.
+// kMasked: the causal mask applies (the diagonal tiles only).
+template <int D, bool kMasked>
+__device__ __forceinline__ void softmax_tile_ref(f32x16 (&sacc)[2], uint32_t key0, uint32_t key_limit,
+                                                 int h, bool first, float &m_run, f32x16 &negm,
+                                                 float &l_run, f32x16 (&oacc)[D / 32],
+                                                 f16x8 (&pop)[4]) {
+    constexpr int NT = D / 32;
+    if constexpr (kMasked) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t key = key0 + 32 * u + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (key > key_limit) sacc[u][i] = -INFINITY;
+            }
+    }
+    // p = 2^(sacc - shift) in fp16, and the lane's sum of those fp16 values
+    // (the row sum uses the probabilities the PV product uses); four
+    // independent sums keep the dependency chains short
+    auto probs = [&](float shift) __attribute__((always_inline)) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            f32x8 v;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = fast_exp2(sacc[st >> 1][8 * (st & 1) + j] - shift);
+            pop[st] = __builtin_convertvector(v, f16x8);
+        }
+        return (sum_f16x8(pop[0], 0.0f) + sum_f16x8(pop[1], 0.0f)) +
+               (sum_f16x8(pop[2], 0.0f) + sum_f16x8(pop[3], 0.0f));
+    };
+    float lt = probs(0.0f);
+    if (__builtin_amdgcn_ballot_w64(first || !(lt <= kPSumMax)) != 0) {
+        // a side effect the compiler may not speculate: the branch stays a
+        // branch instead of being if-converted into every tile's work
+        asm volatile("; softmax reference maximum moves" ::: "memory");
+        float m11[11];
+#pragma unroll
+        for (int j = 0; j < 10; ++j) {
+            const int e = 3 * j;
+            m11[j] = max3_raw(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15],
+                              sacc[(e + 2) >> 4][(e + 2) & 15]);
+        }
+        m11[10] = max3_raw(sacc[1][14], sacc[1][15], sacc[1][15]);
+        const float m4a = max3_raw(m11[0], m11[1], m11[2]);
+        const float m4b = max3_raw(m11[3], m11[4], m11[5]);
+        const float m4c = max3_raw(m11[6], m11[7], m11[8]);
+        const float m4d = max3_raw(m11[9], m11[10], m11[10]);
+        const float mx = xhalf_max(max3_raw(max3_raw(m4a, m4b, m4c), m4d, m4d));
+        // a row whose scores here are all masked has mx = -inf: no shift
+        const float shift = first ? mx : fmaxf(mx, 0.0f);
+        m_run += shift;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negm[i] = -m_run;
+        // (l and O are still 0 on the first tile, whose shift may be any size)
+        const float alpha = first ? 1.0f : fast_exp2(-shift);
+        l_run *= alpha;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[tt][i] *= alpha;
+        lt = probs(shift);
+    }
+    l_run += lt;
 }
 
 // o / l, Qwen3.5 gate (math.rs sigmoid), f32 store; flags non-finite rows.
@@ -1285,21 +1366,24 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     f32x16 oacc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
-    float m_run = -INFINITY;
+    float m_run = 0.0f;  // the reference maximum, set by the first tile
+    f32x16 negm = {};    // -m_run in every element: the S accumulators' start
     float l_run = 0.0f;
     f16x8 pop[4];
     __syncthreads();
     if (grp == 1) __syncthreads();  // group 1 starts one phase later
 
     // one iteration for tile t (t & 1 == PAR): `cur` holds tile t+1 (stored
-    // now), `nxt` receives tile t+2
-    auto step = [&](uint32_t t, auto par, u32x4 (&cur)[SL], u32x4 (&nxt)[SL])
+    // now), `nxt` receives tile t+2.  Unmasked steps (MASKED false) need no
+    // causal mask for tile t and store a whole tile t+1 (not the last).
+    auto step = [&](uint32_t t, auto par, auto masked, u32x4 (&cur)[SL], u32x4 (&nxt)[SL])
                     __attribute__((always_inline)) {
         constexpr uint32_t PAR = decltype(par)::value;
+        constexpr bool MASKED = decltype(masked)::value;
         // ---- M phase: PV(t-1), S(t) ----
         if (t > 0) pv_tile_rows<D>(vbuf + (PAR ^ 1) * kTileBytes<D>, voff, pop, oacc);
         f32x16 sacc[2];
-        s_tile<D>(kbuf + PAR * kTileBytes<D>, qop, h, col, sacc);
+        s_tile<D>(kbuf + PAR * kTileBytes<D>, qop, h, col, sacc, negm);
         __syncthreads();
         // ---- V phase: softmax(t), stage the group's tile t+1, load t+2 ----
         // The page id of tile t+2 (requested one phase earlier) is consumed
@@ -1310,13 +1394,14 @@ attn_prefill_pp_kernel(const PrefillParams p) {
         pin(tb_next);
         pg_next = io.page_of(t + 3);
         const uint32_t key0 = t * kKeyTile;
-        softmax_tile<D>(sacc, key0, key0 + kKeyTile - 1 > first_row_limit, key_limit, h, m_run,
-                        l_run, oacc, pop);
+        softmax_tile_ref<D, MASKED>(sacc, key0, key_limit, h, t == 0, m_run, negm, l_run, oacc,
+                                    pop);
         uint32_t gt = gt0;
         pin(gt);
         if (t + 1 < n) {
             if (grp == 0) io.store_k(cur, kbuf + (PAR ^ 1) * kTileBytes<D>, gt);
-            else io.store_v_rows(cur, vbuf + (PAR ^ 1) * kTileBytes<D>, b.n_keys - key0 - kKeyTile, gt);
+            else io.store_v_rows(cur, vbuf + (PAR ^ 1) * kTileBytes<D>,
+                                 MASKED ? b.n_keys - key0 - kKeyTile : (uint32_t)kKeyTile, gt);
         }
         // issued on every path (past the end, the last tile again): a load
         // skipped on some path would make the next wait for an older load
@@ -1335,11 +1420,21 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     uint32_t t = 0;
     using Even = std::integral_constant<uint32_t, 0>;
     using Odd = std::integral_constant<uint32_t, 1>;
-    for (; t + 1 < n; t += 2) {
-        step(t, Even{}, stage1, stage0);
-        step(t + 1, Odd{}, stage0, stage1);
+    using Whole = std::false_type;
+    using Masked = std::true_type;
+    // tiles every row of the block sees whole and whose successor is not
+    // the last (possibly partial) tile take the unmasked steps; the same
+    // count for both groups, so their barriers still pair up
+    const uint32_t t_main = min((first_row_limit + 1) / kKeyTile, n >= 2 ? n - 2 : 0u);
+    for (; t + 1 < t_main; t += 2) {
+        step(t, Even{}, Whole{}, stage1, stage0);
+        step(t + 1, Odd{}, Whole{}, stage0, stage1);
     }
-    if (t < n) step(t, Even{}, stage1, stage0);
+    for (; t + 1 < n; t += 2) {
+        step(t, Even{}, Masked{}, stage1, stage0);
+        step(t + 1, Odd{}, Masked{}, stage0, stage1);
+    }
+    if (t < n) step(t, Even{}, Masked{}, stage1, stage0);
     pv_tile_rows<D>(vbuf + ((n - 1) & 1) * kTileBytes<D>, voff, pop, oacc);
     if (grp == 0) __syncthreads();  // matches group 1's extra barrier
 
