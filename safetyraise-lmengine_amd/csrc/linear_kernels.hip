@@ -3,29 +3,33 @@
 // (native/cpu/safetyraise_cpu.c:203-239 is the reference: an f32 sum over the
 // columns of each weight row, the weight widened exactly to f32).
 //
-// The weight is widened exactly here too and the products run on
-// v_mfma_f32_16x16x4f32, so every product is an f32 product and only the
-// order of the sum differs from the reference (f32 tolerance, not bf16).
+// Every product is an exact f32 product and only the order of the sum differs
+// from the reference (f32 tolerance, not bf16): f32 and f16 weights are
+// widened exactly and run on v_mfma_f32_16x16x4f32; for bf16 weights x is
+// split exactly into three bf16 parts (split3) that each multiply the stored
+// weight on v_mfma_f32_16x16x32_bf16, 3 MFMAs per 32-k block and tile instead
+// of 8 at a quarter of the rate.
 //
-// Work split.  A workgroup owns 16 rows x 16 outputs and a contiguous range
-// of K; its four waves take quarters of that range and meet in LDS.
-// Decode-sized calls (M <= 16) thus stream every weight row once, which is
-// the HBM-bound regime the ABI's projections live in; each k-step loads 16
-// bytes of x and 8 weight elements per lane and feeds 8 MFMAs.  A call with
-// fewer tiles than kLinWgPerCu workgroups per CU splits K over up to
-// kLinMaxSplits workgroups per tile (grid z): those write partial sums and
-// a second kernel adds them in split order, so results do not depend on
-// timing.
+// Work split.  A workgroup owns 16 rows x 16 T outputs (T tiles per wave)
+// and a contiguous range of K; its W waves take equal parts of that range
+// and meet in LDS.  Decode-sized calls (M <= 16) stream every weight row
+// once, the HBM-bound regime the ABI's projections live in; each k block
+// loads 32 bytes of x per lane, used by T tiles, and 8 weight elements per
+// tile.  x is the larger share of the bytes a lane loads, so T > 1 keeps the
+// load pipeline (texture address unit) from being the limit.  A call whose
+// tiles do not cover the CUs splits K over up to kLinMaxSplits workgroups per
+// tile (grid z): those write partial sums and a second kernel adds them in
+// split order, so results do not depend on timing (linear_plan chooses).
 //
-// Operand order.  For MFMA t of a 32-wide k block, lane (r = lane % 16,
-// g = lane / 16) feeds A = x[row r][k0 + 8g + t] and B = W[output r][same k]:
-// the eight MFMAs cover the block's 32 k values with each lane reading 8
-// consecutive ones (any order of k gives the same sum; A and B share it), so
-// the four lanes of a row read 128 contiguous bytes of x and 64 of a bf16
-// weight row per block.  The accumulator then holds y[row 4g + i][output r]
-// in element i.
+// Operand order.  For a 32-wide k block, lane (r = lane % 16, g = lane / 16)
+// holds x[row r][k0 + 8g .. + 8] and W[output r][same k] (any order of k
+// gives the same sum; A and B share it): the f32 MFMA t takes element t of
+// each, the bf16 MFMA all eight.  The four lanes of a row read 128
+// contiguous bytes of x and 64 of a bf16 weight row per block.  The
+// accumulator then holds y[row 4g + i][output r] in element i.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "sr_internal.hpp"
 #include "sr_device.hpp"
@@ -36,10 +40,10 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kLinTile = 16;   // rows and outputs per workgroup
 constexpr int kLinWaves = 4;   // waves splitting K
-constexpr uint32_t kLinWgPerCu = 1;    // workgroups per CU a call aims for
 constexpr uint32_t kLinMaxSplits = 8;  // K splits per tile at most
 constexpr uint32_t kLinBlock = 32;      // k per block (8 MFMAs)
 constexpr uint32_t kLinMinSplitK = 512;  // K per split at least (4 blocks per wave)
@@ -55,6 +59,25 @@ __device__ __forceinline__ float widen(const void *w, size_t i) {
     }
 }
 
+// Elements i .. i+7 (16-byte aligned for 16-bit types, 32-byte for f32),
+// widened exactly to f32.
+template <int DT>
+__device__ __forceinline__ f32x8 load8_at(const void *base, size_t i) {
+    if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F32) {
+        const f32x4 lo = *(const f32x4 *)((const float *)base + i);
+        const f32x4 hi = *(const f32x4 *)((const float *)base + i + 4);
+        return f32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    } else if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F16) {
+        return __builtin_convertvector(*(const f16x8 *)((const _Float16 *)base + i), f32x8);
+    } else {
+        const uint4 u = *(const uint4 *)((const uint16_t *)base + i);
+        return f32x8{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u),
+                     __uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                     __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
+    }
+}
+
 // Elements k .. k+7 of a row starting at element `row`, those from `lim` on
 // replaced by 0.  The reads themselves are clamped into the row (K >= 1;
 // kVec: K a multiple of 8, so k and lim are too), and the zeros are selected
@@ -66,20 +89,7 @@ __device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k,
                                        uint32_t lim) {
     f32x8 v;
     if constexpr (kVec) {
-        const size_t i = row + min(k, K - 8);
-        if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F32) {
-            const f32x4 lo = *(const f32x4 *)((const float *)base + i);
-            const f32x4 hi = *(const f32x4 *)((const float *)base + i + 4);
-            v = f32x8{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        } else if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_F16) {
-            v = __builtin_convertvector(*(const f16x8 *)((const _Float16 *)base + i), f32x8);
-        } else {
-            const uint4 u = *(const uint4 *)((const uint16_t *)base + i);
-            v = f32x8{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                      __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u),
-                      __uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
-                      __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u)};
-        }
+        v = load8_at<DT>(base, row + min(k, K - 8));
         const bool live = k < lim;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = live ? v[j] : 0.0f;
@@ -93,37 +103,67 @@ __device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k,
     return v;
 }
 
-// y: the output, or (grid z > 1) partial sums [grid z][M][N].  kGroup: k
+// Elements k .. k+7 of a bf16 row as stored (16 bytes), those from `lim` on
+// replaced by 0 (kVec rows; reads clamped into the row as in load8).
+__device__ __forceinline__ bf16x8 load8_bf16(const void *base, size_t row, uint32_t k, uint32_t K,
+                                             uint32_t lim) {
+    uint4 u = *(const uint4 *)((const uint16_t *)base + row + min(k, K - 8));
+    if (!(k < lim)) u = uint4{0, 0, 0, 0};
+    return __builtin_bit_cast(bf16x8, u);
+}
+
+// x as hi + mid + lo in bf16, each the round-to-nearest-even of what the
+// parts before it leave: exact for |x| in [2^-110, bf16's largest finite
+// value] (below, bits under 2^-133 are lost; above, hi is infinite).  With
+// a bf16 weight the three products are then exact f32 products and their
+// sum is w x up to f32 rounding.
+__device__ __forceinline__ void split3(const f32x8 &x, bf16x8 &hi, bf16x8 &mid, bf16x8 &lo) {
+    hi = __builtin_convertvector(x, bf16x8);
+    const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
+    mid = __builtin_convertvector(r1, bf16x8);
+    const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);
+    lo = __builtin_convertvector(r2, bf16x8);
+}
+
+// y: the output, or (grid z > 1) partial sums [grid z][M][N].  T: output tiles per wave (the workgroup owns 16 T
+// outputs; each x fragment a lane loads feeds T MFMAs, so x is read once
+// per 16 T outputs).  W: waves per workgroup, splitting its k range.  kGroup: k
 // blocks per register set (4; 2 for calls with many workgroups per CU, which
-// then hold more waves per SIMD).
-template <int DT, bool kVec, int kGroup>
-__global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, const void *w,
-                                                                 float *y, uint32_t M, uint32_t N,
-                                                                 uint32_t K) {
-    __shared__ f32x4 red[kLinWaves - 1][64];
+// then hold more waves per SIMD).  kExact: every wave's k range is a whole
+// number of pairs of groups of whole blocks (the host checks), so no load
+// reaches past it, nothing is masked and the last pair prefetches nothing.
+template <int DT, bool kVec, int T, int W, int kGroup, bool kExact>
+__global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const void *w, float *y,
+                                                        uint32_t M, uint32_t N, uint32_t K) {
+    static_assert(!kExact || kVec, "exact ranges use the vector loads");
+    __shared__ f32x4 red[W - 1][T][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const uint32_t r = lane & 15, g = lane >> 4;
-    const uint32_t n0 = blockIdx.x * kLinTile, m0 = blockIdx.y * kLinTile;
+    const uint32_t n0 = blockIdx.x * kLinTile * T, m0 = blockIdx.y * kLinTile;
     // rows past M / N read the last row and their results are not stored
     if (K == 0) {  // empty sums (uniform): zeros
         if (wave == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t m = m0 + 4 * g + i, n = n0 + r;
-                if (m < M && n < N) y[(size_t)m * N + n] = 0.0f;
-            }
+            for (int u = 0; u < T; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t m = m0 + 4 * g + i, n = n0 + kLinTile * u + r;
+                    if (m < M && n < N) y[(size_t)m * N + n] = 0.0f;
+                }
         }
         return;
     }
     const size_t xrow = (size_t)min(m0 + r, M - 1) * K;
-    const size_t wrow = (size_t)min(n0 + r, N - 1) * K;
+    size_t wrow[T];
+#pragma unroll
+    for (int u = 0; u < T; ++u) wrow[u] = (size_t)min(n0 + kLinTile * u + r, N - 1) * K;
     y += (size_t)blockIdx.z * M * N;
     const uint32_t nblk = (K + kLinBlock - 1) / kLinBlock;
     const uint32_t s0 = (uint32_t)((uint64_t)nblk * blockIdx.z / gridDim.z);
     const uint32_t s1 = (uint32_t)((uint64_t)nblk * (blockIdx.z + 1) / gridDim.z);
-    const uint32_t b0 = s0 + (uint32_t)((uint64_t)(s1 - s0) * wave / kLinWaves);
-    const uint32_t b1 = s0 + (uint32_t)((uint64_t)(s1 - s0) * (wave + 1) / kLinWaves);
+    const uint32_t b0 = s0 + (uint32_t)((uint64_t)(s1 - s0) * wave / W);
+    const uint32_t b1 = s0 + (uint32_t)((uint64_t)(s1 - s0) * (wave + 1) / W);
     // this wave's k range ends at kend: loads past it read zeros, so a group
     // that runs past the range adds nothing (and no block is counted twice)
     const uint32_t kend = min(kLinBlock * b1, K);
@@ -131,55 +171,121 @@ __global__ __launch_bounds__(64 * kLinWaves) void linear_kernel(const float *x, 
     // set run, the loads of the other are in flight (the sets alternate
     // explicitly, so the compiler cannot merge them into one and wait for
     // loads it has just issued)
-    f32x8 xa[kGroup], wa[kGroup], xb[kGroup], wb[kGroup];
-    auto load_group = [&](uint32_t b, f32x8 (&xv)[kGroup], f32x8 (&wv)[kGroup])
+    // kSplit (bf16 weights): the weight stays bf16 and x is split in three
+    // bf16 parts, so a 32-k block takes 3 v_mfma_f32_16x16x32_bf16 per tile
+    // instead of 8 v_mfma_f32_16x16x4f32
+    constexpr bool kSplit = DT == SAFETYRAISE_KERNEL_DTYPE_BF16 && kVec;
+    using WV = std::conditional_t<kSplit, bf16x8, f32x8>;
+    f32x8 xa[kGroup], xb[kGroup];
+    WV wa[kGroup][T], wb[kGroup][T];
+    auto load_group = [&](uint32_t b, f32x8 (&xv)[kGroup], WV (&wv)[kGroup][T])
                           __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kGroup; ++j) {
             const uint32_t k = kLinBlock * (b + j) + 8 * g;
-            xv[j] = load8<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K, kend);
-            wv[j] = load8<DT, kVec>(w, wrow, k, K, kend);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // four accumulation chains (MFMA t of a block feeds chain t % 4), so
-    // consecutive MFMAs do not wait for each other's results
-    constexpr int kChains = 4;
-    f32x4 acc4[kChains];
+            if constexpr (kExact) {
+                xv[j] = load8_at<SAFETYRAISE_KERNEL_DTYPE_F32>(x, xrow + k);
+            } else {
+                xv[j] = load8<SAFETYRAISE_KERNEL_DTYPE_F32, kVec>(x, xrow, k, K, kend);
+            }
 #pragma unroll
-    for (int c = 0; c < kChains; ++c) acc4[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mfma_group = [&](const f32x8 (&xv)[kGroup], const f32x8 (&wv)[kGroup])
-                          __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                f32x4 &a = acc4[t % kChains];
-                a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][t], wv[j][t], a, 0, 0, 0);
+            for (int u = 0; u < T; ++u) {
+                if constexpr (kSplit && kExact) {
+                    wv[j][u] = *(const bf16x8 *)((const uint16_t *)w + wrow[u] + k);
+                } else if constexpr (kSplit) {
+                    wv[j][u] = load8_bf16(w, wrow[u], k, K, kend);
+                } else if constexpr (kExact) {
+                    wv[j][u] = load8_at<DT>(w, wrow[u] + k);
+                } else {
+                    wv[j][u] = load8<DT, kVec>(w, wrow[u], k, K, kend);
+                }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     };
-    // groups past the range load zeros (clamped reads) and add nothing
+    // kChains accumulation chains per tile (MFMA t of a block feeds chain
+    // t % kChains, or one chain per part of x), so consecutive MFMAs do not
+    // wait for each other's results
+    constexpr int kChains = kSplit ? 3 : (T == 1 ? 4 : 2);
+    f32x4 acc4[T][kChains];
+#pragma unroll
+    for (int u = 0; u < T; ++u)
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) acc4[u][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mfma_group = [&](const f32x8 (&xv)[kGroup], const WV (&wv)[kGroup][T])
+                          __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            if constexpr (kSplit) {
+                bf16x8 part[3];
+                split3(xv[j], part[0], part[1], part[2]);
+#pragma unroll
+                for (int c = 0; c < 3; ++c)
+#pragma unroll
+                    for (int u = 0; u < T; ++u)
+                        acc4[u][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(part[c], wv[j][u],
+                                                                             acc4[u][c], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+#pragma unroll
+                    for (int u = 0; u < T; ++u) {
+                        f32x4 &a = acc4[u][t % kChains];
+                        a = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][t], wv[j][u][t], a, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
     load_group(b0, xa, wa);
-    for (uint32_t b = b0; b < b1; b += 2 * kGroup) {
+    if constexpr (kExact) {
+        // b1 - b0 is a positive multiple of 2 kGroup: the last pair loads
+        // nothing past b1
+        uint32_t b = b0;
+        for (; b + 2 * kGroup < b1; b += 2 * kGroup) {
+            load_group(b + kGroup, xb, wb);
+            mfma_group(xa, wa);
+            load_group(b + 2 * kGroup, xa, wa);
+            mfma_group(xb, wb);
+        }
         load_group(b + kGroup, xb, wb);
         mfma_group(xa, wa);
-        load_group(b + 2 * kGroup, xa, wa);
         mfma_group(xb, wb);
+    } else {
+        // groups past the range load zeros (clamped reads) and add nothing
+        for (uint32_t b = b0; b < b1; b += 2 * kGroup) {
+            load_group(b + kGroup, xb, wb);
+            mfma_group(xa, wa);
+            load_group(b + 2 * kGroup, xa, wa);
+            mfma_group(xb, wb);
+        }
     }
-    const f32x4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-    if (wave > 0) red[wave - 1][lane] = acc;
+    // the chains summed last to first (with split x: lo + mid, then hi)
+    f32x4 acc[T];
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+        acc[u] = acc4[u][kChains - 1];
+#pragma unroll
+        for (int c = kChains - 2; c >= 0; --c) acc[u] += acc4[u][c];
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int u = 0; u < T; ++u) red[wave - 1][u][lane] = acc[u];
+    }
     __syncthreads();
     if (wave != 0) return;
-    f32x4 sum = acc;
 #pragma unroll
-    for (int j = 0; j < kLinWaves - 1; ++j) sum += red[j][lane];
-    const uint32_t n = n0 + r;
+    for (int u = 0; u < T; ++u) {
+        f32x4 sum = acc[u];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t m = m0 + 4 * g + i;
-        if (m < M && n < N) y[(size_t)m * N + n] = sum[i];
+        for (int j = 0; j < W - 1; ++j) sum += red[j][u][lane];
+        const uint32_t n = n0 + kLinTile * u + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = m0 + 4 * g + i;
+            if (m < M && n < N) y[(size_t)m * N + n] = sum[i];
+        }
     }
 }
 
@@ -198,48 +304,92 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
     y[i] = s;
 }
 
-template <int DT, int kGroup>
+// How a call is cut: T output tiles per wave, W waves per workgroup and K
+// split over `splits` workgroups per tile (their partial sums are added by
+// a second kernel, in split order), never more workgroups than CUs (one
+// 8-wave workgroup fills a CU: one more would take a second round).  T = 3
+// or, for bf16 weights, 4 (x read once per 48 or 64 outputs, 8 waves: two
+// per SIMD; wider weights take more registers than a wave has) when its
+// workgroups cover 7/8 of the CUs without a split, or with one when the
+// weight is large enough (kLinSplitTElems) that the second kernel's few
+// microseconds are small against the stream; otherwise one tile per wave
+// and 4 waves, K split until the CUs are covered.
+constexpr uint64_t kLinSplitTElems = (uint64_t)32 << 20;
+struct LinPlan {
+    uint32_t T, W, splits;
+};
+LinPlan linear_plan(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
+    const uint64_t cus = (uint64_t)(num_cus > 0 ? num_cus : 1);
+    const uint64_t mt = (M + kLinTile - 1) / kLinTile;
+    auto splits_for = [&](uint64_t tiles) -> uint32_t {
+        if (tiles == 0 || tiles >= cus) return 1;
+        uint64_t s = cus / tiles;
+        s = std::min<uint64_t>(s, K / kLinMinSplitK);
+        s = std::min<uint64_t>(s, kLinMaxSplits);
+        return s < 1 ? 1u : (uint32_t)s;
+    };
+    const uint32_t t_max = dtype == SAFETYRAISE_KERNEL_DTYPE_BF16 ? 4 : 3;
+    for (uint32_t T = 3; T <= t_max; ++T) {
+        const uint64_t t = (uint64_t)((N + T * kLinTile - 1) / (T * kLinTile)) * mt;
+        const uint32_t s = splits_for(t);
+        if (t * s * 8 >= cus * 7 && (s == 1 || (uint64_t)N * K >= kLinSplitTElems)) {
+            return {T, 8, s};
+        }
+    }
+    const uint64_t t1 = (uint64_t)((N + kLinTile - 1) / kLinTile) * mt;
+    return {1, kLinWaves, splits_for(t1)};
+}
+
+template <int DT, int T, int W, int kGroup>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
                uint32_t K, uint32_t splits) {
-    const dim3 grid((N + kLinTile - 1) / kLinTile, (M + kLinTile - 1) / kLinTile, splits);
+    const dim3 grid((N + kLinTile * T - 1) / (kLinTile * T), (M + kLinTile - 1) / kLinTile, splits);
     // 16-byte loads need 16-byte aligned rows: K a multiple of 8 and x itself
     // aligned (a device caller may pass a view that starts mid-vector; the
     // weight is the plugin's own allocation)
     if ((K & 7u) == 0 && ((uintptr_t)x & 15u) == 0) {
-        SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, kGroup>), grid, dim3(64 * kLinWaves), 0,
-                  stream, x, w, y, M, N, K);
+        // every wave gets the same whole number of pairs of groups
+        const bool exact = K % kLinBlock == 0 &&
+                           (K / kLinBlock) % (splits * (uint32_t)W * 2u * (uint32_t)kGroup) == 0;
+        if (exact) {
+            SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, T, W, kGroup, true>), grid,
+                      dim3(64 * W), 0, stream, x, w, y, M, N, K);
+        } else {
+            SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, T, W, kGroup, false>), grid,
+                      dim3(64 * W), 0, stream, x, w, y, M, N, K);
+        }
     } else {
-        SR_LAUNCH("linear_kernel", (linear_kernel<DT, false, kGroup>), grid, dim3(64 * kLinWaves), 0,
-                  stream, x, w, y, M, N, K);
+        SR_LAUNCH("linear_kernel", (linear_kernel<DT, false, T, W, kGroup, false>), grid,
+                  dim3(64 * W), 0, stream, x, w, y, M, N, K);
     }
 }
 
 template <int DT>
-void launch_dt_groups(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M,
-                      uint32_t N, uint32_t K, uint32_t splits, int num_cus) {
+void launch_dt_plan(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M,
+                    uint32_t N, uint32_t K, const LinPlan &plan, int num_cus) {
+    if (plan.T == 3) {
+        launch_dt<DT, 3, 8, 2>(stream, x, w, y, M, N, K, plan.splits);
+        return;
+    }
+    if constexpr (DT == SAFETYRAISE_KERNEL_DTYPE_BF16) {
+        if (plan.T == 4) {
+            launch_dt<DT, 4, 8, 2>(stream, x, w, y, M, N, K, plan.splits);
+            return;
+        }
+    }
     const uint64_t wgs = (uint64_t)((N + kLinTile - 1) / kLinTile) * ((M + kLinTile - 1) / kLinTile) *
-                         splits;
+                         plan.splits;
     if (wgs >= 2 * (uint64_t)(num_cus > 0 ? num_cus : 1)) {
-        launch_dt<DT, 2>(stream, x, w, y, M, N, K, splits);
+        launch_dt<DT, 1, kLinWaves, 2>(stream, x, w, y, M, N, K, plan.splits);
     } else {
-        launch_dt<DT, 4>(stream, x, w, y, M, N, K, splits);
+        launch_dt<DT, 1, kLinWaves, 4>(stream, x, w, y, M, N, K, plan.splits);
     }
 }
 
 }  // namespace
 
-uint32_t linear_splits(uint32_t M, uint32_t N, uint32_t K, int num_cus) {
-    const uint64_t tiles = (uint64_t)((N + kLinTile - 1) / kLinTile) * ((M + kLinTile - 1) / kLinTile);
-    const uint64_t target = (uint64_t)kLinWgPerCu * (uint64_t)(num_cus > 0 ? num_cus : 1);
-    if (tiles == 0 || tiles >= target) return 1;
-    uint64_t s = (target + tiles - 1) / tiles;
-    s = std::min<uint64_t>(s, K / kLinMinSplitK);
-    s = std::min<uint64_t>(s, kLinMaxSplits);
-    return s < 1 ? 1u : (uint32_t)s;
-}
-
-size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, int num_cus) {
-    const uint32_t s = linear_splits(M, N, K, num_cus);
+size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
+    const uint32_t s = linear_plan(M, N, K, dtype, num_cus).splits;
     return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
@@ -262,24 +412,25 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
         }
         return hipSuccess;
     }
-    const uint32_t splits = linear_splits(M, N, K, num_cus);
+    const LinPlan plan = linear_plan(M, N, K, dtype, num_cus);
+    const uint32_t splits = plan.splits;
     if (splits > 1 && scratch == nullptr) return hipErrorInvalidValue;
     float *dst = splits > 1 ? scratch : y;
     switch (dtype) {
         case SAFETYRAISE_KERNEL_DTYPE_F32:
-            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, dst, M, N, K, splits, num_cus);
+            launch_dt_plan<SAFETYRAISE_KERNEL_DTYPE_F32>(stream, x, w, dst, M, N, K, plan, num_cus);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_F16:
-            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, dst, M, N, K, splits, num_cus);
+            launch_dt_plan<SAFETYRAISE_KERNEL_DTYPE_F16>(stream, x, w, dst, M, N, K, plan, num_cus);
             break;
         case SAFETYRAISE_KERNEL_DTYPE_BF16:
-            launch_dt_groups<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, dst, M, N, K, splits, num_cus);
+            launch_dt_plan<SAFETYRAISE_KERNEL_DTYPE_BF16>(stream, x, w, dst, M, N, K, plan, num_cus);
             break;
         default:
             return hipErrorInvalidValue;
     }
     if (splits > 1) {
-        // splits > 1 only when tiles < kLinWgPerCu * CUs, so M * N is small
+        // splits > 1 only when the tiles do not cover the CUs, so M * N is small
         const uint32_t count = M * N;
         SR_LAUNCH("linear_split_sum_kernel", linear_split_sum_kernel, dim3((count + 255) / 256),
                   dim3(256), 0, stream, scratch, y, count, splits);

@@ -337,7 +337,7 @@ static int32_t check_linear(Ctx *ctx, const safetyraise_kernel_weight *w, const 
 static int32_t linear_scratch(Ctx *ctx, const safetyraise_kernel_weight *w, uint64_t rows,
                               float **part) {
     const size_t bytes = linear_scratch_bytes((uint32_t)rows, (uint32_t)w->rows,
-                                              (uint32_t)w->cols, ctx->num_cus);
+                                              (uint32_t)w->cols, w->dtype, ctx->num_cus);
     *part = nullptr;
     if (bytes == 0) return kOk;
     const int32_t e = ensure_buffer(ctx, ctx->linear_part, bytes, false);

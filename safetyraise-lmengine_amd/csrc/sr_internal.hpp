@@ -331,10 +331,10 @@ struct GdnRollback {
 };
 hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r);
 
-// y[M][N] = x[M][K] . W[N][K]^T on f32 MFMA, W of dtype F32/F16/BF16
+// y[M][N] = x[M][K] . W[N][K]^T with f32 products, W of dtype F32/F16/BF16
 // (linear_kernels.hip).  scratch holds linear_scratch_bytes(...) bytes of
 // partial sums (none when that is 0) for calls that split K.
-size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, int num_cus);
+size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus);
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
                          float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
                          int num_cus);

@@ -2,15 +2,17 @@
 
 linear computes output[r][o] = sum_c input[r][c] * weight[o][c] in f32 with
 the weight widened exactly from F32, F16 or BF16.  The plugin sums in another
-order (f32 MFMA over k blocks, four partial sums), so random inputs are held
-to |d| <= 1e-5 * sum_c |input * weight| + 1e-4 * |ref| (the error bound of a
-reordered f32 sum scales with the magnitude of the terms, not of the result),
-and integer-valued inputs, whose every partial sum is exact in f32, must match
-the oracle bit for bit.  Calls with few output tiles split K over several
-workgroups whose partial sums a second kernel adds (shapes (1, 4096, 512),
-(3, 2001, 100), (5, 1030, 20) and the 3072-column device call do); calls with
-at least two workgroups per CU ((16, 512, 8192), (32, 130, 4100)) keep two k
-blocks per register set instead of four.
+order (f32 MFMA over k blocks, or for bf16 weights x split exactly into three
+bf16 parts on the bf16 MFMA, with partial sums per chain and wave), so random
+inputs are held to |d| <= 1e-5 * sum_c |input * weight| + 1e-4 * |ref| (the
+error bound of a reordered f32 sum scales with the magnitude of the terms, not
+of the result), and integer-valued inputs, whose every partial sum is exact in
+f32, must match the oracle bit for bit.  Calls with few output tiles split K
+over several workgroups whose partial sums a second kernel adds (shapes
+(1, 4096, 512), (3, 2001, 100), (5, 1030, 20), the 3072-column device call and
+two of the projection shapes do); calls with at least two workgroups per CU
+((16, 512, 8192), (32, 130, 4100)) keep two k blocks per register set instead
+of four.
 """
 import ctypes as C
 
@@ -103,6 +105,28 @@ def test_integer_inputs_are_bit_exact(backend, rng, dtype):
     w = rng.integers(-8, 9, size=(70, 515)).astype(np.float32)
     bits = weight_bits(w, dtype)
     assert np.array_equal(backend.linear(bits, x, dtype), O.linear(x, bits, dtype))
+
+
+@pytest.mark.parametrize("rows,cols,out", [(16, 4096, 12288), (16, 12288, 4096), (16, 4096, 4096),
+                                           (16, 4096, 1024)])
+def test_projection_shapes_integer_inputs_bit_exact(backend, rng, rows, cols, out):
+    # Qwen3-8B's projection shapes at 16 rows cover the ways a call is cut:
+    # three output tiles per wave unsplit (gate/up) and with K split over
+    # three workgroups (down), one tile per wave unsplit (q/o) and with K
+    # split (k/v).  Integer inputs keep every partial sum exact, so any order
+    # must equal the reference bit for bit; the second call reuses the
+    # partial-sum scratch.
+    x = rng.integers(-8, 9, size=(rows, cols)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(out, cols)).astype(np.float32)
+    bits = weight_bits(w, BF16)
+    prepared = backend.create_weight(bits, BF16)
+    try:
+        ref = O.linear(x, bits, BF16)
+        assert np.array_equal(backend.linear(prepared, x), ref)
+        x2 = x[::-1].copy()
+        assert np.array_equal(backend.linear(prepared, x2), O.linear(x2, bits, BF16))
+    finally:
+        prepared.destroy()
 
 
 @pytest.mark.parametrize("cols", [256, 3072])  # 3072: K split over workgroups
