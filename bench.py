@@ -453,6 +453,7 @@ def cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim, chunk):
 
 
 MFMA_F32_PEAK_TFS = 157.3  # MI355X dense fp32 matrix
+GDN_KERNEL_CHUNK = 32  # rows per chunk of gdn_chunk_kernel (kCk in gdn_kernels.hip)
 
 
 def gdn_layer_setup(torch, pkg, backend, gen, hk, hv, dk, dv, K, nseq):
@@ -667,10 +668,10 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
     flops = 7 * dk * dv * hv * nseq * total
     tflops = flops / (ms * 1e-3) / 1e12
     # the roofline's algorithmic count: the chunked (WY) form's FLOPs at the
-    # call's chunk of C = 64 rows, 4 C^2 Dk + 2/3 C^3 + 4 C^2 Dv + 8 C Dk Dv +
-    # 2 C^2 Dv per (sequence, value head, chunk); the token-serial count is
-    # reported beside it
-    ck = chunk
+    # chunk the kernel runs, C = 32 rows (each 64-row call is two chunks):
+    # 4 C^2 Dk + 2/3 C^3 + 4 C^2 Dv + 8 C Dk Dv + 2 C^2 Dv per (sequence, value
+    # head, chunk); the token-serial count is reported beside it
+    ck = GDN_KERNEL_CHUNK
     chunked_form = ((4 * ck * ck * dk + 2 * ck ** 3 / 3 + 4 * ck * ck * dv + 8 * ck * dk * dv
                      + 2 * ck * ck * dv) * nseq * hv * (total // ck))
     chunk_us = kernels["gdn_chunk_kernel"]["us"]

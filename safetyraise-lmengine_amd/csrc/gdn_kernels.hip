@@ -382,6 +382,13 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     const bool keep = a.records != nullptr;  // uniform
     const uint32_t hv_dv = a.value_heads * kHeadDv;
     const bool owns_qk = (h % groups == 0);
+    // the remaining small inputs are requested before the state: loads
+    // complete in order for the wait counter, so a wait for one requested
+    // after the state would wait for the whole state too, and the conv and
+    // norms could no longer run while the state arrives
+    const float a_log_v = a.a_log[h];
+    const float dt = a.dt_bias[h];
+    const float nw0 = a.norm[lane], nw1 = a.norm[lane + 64];
     // the state is read once and written once per call: nontemporal
     // accesses (streaming reads measured ~8 % faster than ordinary loads)
     typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
@@ -394,10 +401,8 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
         S[i][0] = x0.x; S[i][1] = x0.y; S[i][2] = x0.z; S[i][3] = x0.w;
         S[i][4] = x1.x; S[i][5] = x1.y; S[i][6] = x1.z; S[i][7] = x1.w;
     }
-    const float a_log_e = expf(a.a_log[h]);
-    const float dt = a.dt_bias[h];
+    const float a_log_e = expf(a_log_v);
     const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:213
-    const float nw0 = a.norm[lane], nw1 = a.norm[lane + 64];
     __syncthreads();
 
     for (uint32_t r = 0; r < m.rows; ++r) {
