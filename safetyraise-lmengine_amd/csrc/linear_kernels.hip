@@ -10,6 +10,15 @@
 // weight on v_mfma_f32_16x16x32_bf16, 3 MFMAs per 32-k block and tile instead
 // of 8 at a quarter of the rate.
 //
+// Weight layout.  F32 and F16 weights stay row-major as given.  A BF16 weight
+// is repacked once, when its handle is created (linear_pack_weight), into
+// 1 KB tiles: for output tile t (16 rows) and k block b (32 columns) the 512
+// elements from (t * nblk + b) * 512 on hold, at 8 (16 g + r), W[16 t + r]
+// [32 b + 8 g .. + 8], with zeros past N and K.  Lane (r, g) then loads its
+// operand as 16 contiguous bytes, one load instruction reads 1 KB of
+// contiguous memory instead of 64 bytes of 16 rows, and every call reads
+// aligned whole blocks whatever its shape.
+//
 // Work split.  A workgroup owns 16 rows x 16 T outputs (T tiles per wave)
 // and a contiguous range of K; its W waves take equal parts of that range
 // and meet in LDS.  Decode-sized calls (M <= 16) stream every weight row
@@ -25,8 +34,8 @@
 // holds x[row r][k0 + 8g .. + 8] and W[output r][same k] (any order of k
 // gives the same sum; A and B share it): the f32 MFMA t takes element t of
 // each, the bf16 MFMA all eight.  The four lanes of a row read 128
-// contiguous bytes of x and 64 of a bf16 weight row per block.  The
-// accumulator then holds y[row 4g + i][output r] in element i.
+// contiguous bytes of x per block.  The accumulator then holds
+// y[row 4g + i][output r] in element i.
 
 #include <algorithm>
 #include <type_traits>
@@ -103,15 +112,6 @@ __device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k,
     return v;
 }
 
-// Elements k .. k+7 of a bf16 row as stored (16 bytes), those from `lim` on
-// replaced by 0 (kVec rows; reads clamped into the row as in load8).
-__device__ __forceinline__ bf16x8 load8_bf16(const void *base, size_t row, uint32_t k, uint32_t K,
-                                             uint32_t lim) {
-    uint4 u = *(const uint4 *)((const uint16_t *)base + row + min(k, K - 8));
-    if (!(k < lim)) u = uint4{0, 0, 0, 0};
-    return __builtin_bit_cast(bf16x8, u);
-}
-
 // x as hi + mid + lo in bf16, each the round-to-nearest-even of what the
 // parts before it leave: exact for |x| in [2^-110, bf16's largest finite
 // value] (below, bits under 2^-133 are lost; above, hi is infinite).  With
@@ -154,12 +154,25 @@ __global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const vo
         }
         return;
     }
+    // kTiled (bf16 weights): the weight is in 1 KB tiles; x is split in
+    // three bf16 parts, so a 32-k block takes 3 v_mfma_f32_16x16x32_bf16 per
+    // tile instead of 8 v_mfma_f32_16x16x4f32
+    constexpr bool kTiled = DT == SAFETYRAISE_KERNEL_DTYPE_BF16;
+    const uint32_t nblk = (K + kLinBlock - 1) / kLinBlock;
     const size_t xrow = (size_t)min(m0 + r, M - 1) * K;
+    // row-major weights: the row of output r of each tile; tiled: this
+    // lane's 16 bytes in block 0 of each tile (tiles past N read the last)
     size_t wrow[T];
 #pragma unroll
-    for (int u = 0; u < T; ++u) wrow[u] = (size_t)min(n0 + kLinTile * u + r, N - 1) * K;
+    for (int u = 0; u < T; ++u) {
+        if constexpr (kTiled) {
+            const uint32_t tile = min(n0 / kLinTile + u, (N - 1) / kLinTile);
+            wrow[u] = (size_t)tile * nblk * 512 + (size_t)lane * 8;
+        } else {
+            wrow[u] = (size_t)min(n0 + kLinTile * u + r, N - 1) * K;
+        }
+    }
     y += (size_t)blockIdx.z * M * N;
-    const uint32_t nblk = (K + kLinBlock - 1) / kLinBlock;
     const uint32_t s0 = (uint32_t)((uint64_t)nblk * blockIdx.z / gridDim.z);
     const uint32_t s1 = (uint32_t)((uint64_t)nblk * (blockIdx.z + 1) / gridDim.z);
     const uint32_t b0 = s0 + (uint32_t)((uint64_t)(s1 - s0) * wave / W);
@@ -171,11 +184,7 @@ __global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const vo
     // set run, the loads of the other are in flight (the sets alternate
     // explicitly, so the compiler cannot merge them into one and wait for
     // loads it has just issued)
-    // kSplit (bf16 weights): the weight stays bf16 and x is split in three
-    // bf16 parts, so a 32-k block takes 3 v_mfma_f32_16x16x32_bf16 per tile
-    // instead of 8 v_mfma_f32_16x16x4f32
-    constexpr bool kSplit = DT == SAFETYRAISE_KERNEL_DTYPE_BF16 && kVec;
-    using WV = std::conditional_t<kSplit, bf16x8, f32x8>;
+    using WV = std::conditional_t<kTiled, bf16x8, f32x8>;
     f32x8 xa[kGroup], xb[kGroup];
     WV wa[kGroup][T], wb[kGroup][T];
     auto load_group = [&](uint32_t b, f32x8 (&xv)[kGroup], WV (&wv)[kGroup][T])
@@ -190,10 +199,16 @@ __global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const vo
             }
 #pragma unroll
             for (int u = 0; u < T; ++u) {
-                if constexpr (kSplit && kExact) {
-                    wv[j][u] = *(const bf16x8 *)((const uint16_t *)w + wrow[u] + k);
-                } else if constexpr (kSplit) {
-                    wv[j][u] = load8_bf16(w, wrow[u], k, K, kend);
+                if constexpr (kTiled && kExact) {
+                    wv[j][u] = *(const bf16x8 *)((const uint16_t *)w + wrow[u] +
+                                                 (size_t)(b + j) * 512);
+                } else if constexpr (kTiled) {
+                    // blocks past this wave's range: read the last block of
+                    // the tile, add zeros (selected after the load)
+                    uint4 v = *(const uint4 *)((const uint16_t *)w + wrow[u] +
+                                               (size_t)min(b + j, nblk - 1) * 512);
+                    if (!(b + j < b1)) v = uint4{0, 0, 0, 0};
+                    wv[j][u] = __builtin_bit_cast(bf16x8, v);
                 } else if constexpr (kExact) {
                     wv[j][u] = load8_at<DT>(w, wrow[u] + k);
                 } else {
@@ -206,7 +221,7 @@ __global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const vo
     // kChains accumulation chains per tile (MFMA t of a block feeds chain
     // t % kChains, or one chain per part of x), so consecutive MFMAs do not
     // wait for each other's results
-    constexpr int kChains = kSplit ? 3 : (T == 1 ? 4 : 2);
+    constexpr int kChains = kTiled ? 3 : (T == 1 ? 4 : 2);
     f32x4 acc4[T][kChains];
 #pragma unroll
     for (int u = 0; u < T; ++u)
@@ -216,7 +231,7 @@ __global__ __launch_bounds__(64 * W) void linear_kernel(const float *x, const vo
                           __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kGroup; ++j) {
-            if constexpr (kSplit) {
+            if constexpr (kTiled) {
                 bf16x8 part[3];
                 split3(xv[j], part[0], part[1], part[2]);
 #pragma unroll
@@ -304,6 +319,28 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
     y[i] = s;
 }
 
+// The bf16 tile layout from a row-major [N][K] weight: thread c writes the
+// 16 bytes lane c % 64 loads from tile block c / 64 (blocks in tile-major
+// order, nblk per tile), zeros past N and K.
+__global__ __launch_bounds__(256) void linear_pack_bf16_kernel(const uint16_t *src, uint16_t *dst,
+                                                               uint64_t N, uint64_t K, uint64_t nblk,
+                                                               uint64_t chunks) {
+    const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const uint64_t lane = c & 63, tb = c >> 6;
+    const uint64_t n = kLinTile * (tb / nblk) + (lane & 15);
+    const uint64_t k0 = kLinBlock * (tb % nblk) + 8 * (lane >> 4);
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint64_t ka = k0 + 2 * i;
+        const uint32_t lo = n < N && ka < K ? src[n * K + ka] : 0u;
+        const uint32_t hi = n < N && ka + 1 < K ? src[n * K + ka + 1] : 0u;
+        p[i] = lo | (hi << 16);
+    }
+    *(uint4 *)(dst + c * 8) = uint4{p[0], p[1], p[2], p[3]};
+}
+
 // How a call is cut: T output tiles per wave, W waves per workgroup and K
 // split over `splits` workgroups per tile (their partial sums are added by
 // a second kernel, in split order), never more workgroups than CUs (one
@@ -344,6 +381,10 @@ template <int DT, int T, int W, int kGroup>
 void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint32_t M, uint32_t N,
                uint32_t K, uint32_t splits) {
     const dim3 grid((N + kLinTile * T - 1) / (kLinTile * T), (M + kLinTile - 1) / kLinTile, splits);
+    // the kernel timer's label names the plan (tiles per wave, K split)
+    const char *name = T == 3   ? "linear_kernel_t3"
+                       : T == 4 ? "linear_kernel_t4"
+                                : (splits > 1 ? "linear_kernel_t1_split" : "linear_kernel_t1");
     // 16-byte loads need 16-byte aligned rows: K a multiple of 8 and x itself
     // aligned (a device caller may pass a view that starts mid-vector; the
     // weight is the plugin's own allocation)
@@ -352,15 +393,15 @@ void launch_dt(hipStream_t stream, const float *x, const void *w, float *y, uint
         const bool exact = K % kLinBlock == 0 &&
                            (K / kLinBlock) % (splits * (uint32_t)W * 2u * (uint32_t)kGroup) == 0;
         if (exact) {
-            SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, T, W, kGroup, true>), grid,
-                      dim3(64 * W), 0, stream, x, w, y, M, N, K);
+            SR_LAUNCH(name, (linear_kernel<DT, true, T, W, kGroup, true>), grid, dim3(64 * W), 0,
+                      stream, x, w, y, M, N, K);
         } else {
-            SR_LAUNCH("linear_kernel", (linear_kernel<DT, true, T, W, kGroup, false>), grid,
-                      dim3(64 * W), 0, stream, x, w, y, M, N, K);
+            SR_LAUNCH(name, (linear_kernel<DT, true, T, W, kGroup, false>), grid, dim3(64 * W), 0,
+                      stream, x, w, y, M, N, K);
         }
     } else {
-        SR_LAUNCH("linear_kernel", (linear_kernel<DT, false, T, W, kGroup, false>), grid,
-                  dim3(64 * W), 0, stream, x, w, y, M, N, K);
+        SR_LAUNCH(name, (linear_kernel<DT, false, T, W, kGroup, false>), grid, dim3(64 * W), 0,
+                  stream, x, w, y, M, N, K);
     }
 }
 
@@ -387,6 +428,37 @@ void launch_dt_plan(hipStream_t stream, const float *x, const void *w, float *y,
 }
 
 }  // namespace
+
+size_t linear_weight_bytes(uint64_t rows, uint64_t cols, uint32_t dtype) {
+    uint64_t n = 0, bytes = 0;
+    if (dtype == SAFETYRAISE_KERNEL_DTYPE_BF16) {
+        // whole tiles of 16 rows x 32 columns
+        const uint64_t tiles = (rows + kLinTile - 1) / kLinTile;
+        const uint64_t blocks = (cols + kLinBlock - 1) / kLinBlock;
+        if (__builtin_mul_overflow(tiles, blocks, &n) || __builtin_mul_overflow(n, 1024u, &bytes)) {
+            return SIZE_MAX;
+        }
+        return (size_t)bytes;
+    }
+    const uint64_t element = dtype == SAFETYRAISE_KERNEL_DTYPE_F32 ? 4 : 2;
+    if (__builtin_mul_overflow(rows, cols, &n) || __builtin_mul_overflow(n, element, &bytes)) {
+        return SIZE_MAX;
+    }
+    return (size_t)bytes;
+}
+
+hipError_t linear_pack_bf16(hipStream_t stream, const void *src, void *dst, uint64_t rows,
+                            uint64_t cols) {
+    const uint64_t nblk = (cols + kLinBlock - 1) / kLinBlock;
+    const uint64_t chunks = (rows + kLinTile - 1) / kLinTile * nblk * 64;
+    if (chunks == 0) return hipSuccess;
+    const uint64_t blocks = (chunks + 255) / 256;
+    if (blocks > 0x7fffffffu) return hipErrorInvalidValue;
+    SR_LAUNCH("linear_pack_bf16_kernel", linear_pack_bf16_kernel, dim3((uint32_t)blocks),
+              dim3(256), 0, stream, (const uint16_t *)src, (uint16_t *)dst, rows, cols, nblk,
+              chunks);
+    return hipGetLastError();
+}
 
 size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
     const uint32_t s = linear_plan(M, N, K, dtype, num_cus).splits;

@@ -288,8 +288,24 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_create_weight(
     weight->cols = cols;
     weight->dtype = dtype;
     if (bytes != 0) {
-        hipError_t e = hipMalloc(&weight->d_data, bytes);
-        if (e == hipSuccess) e = hipMemcpy(weight->d_data, data, bytes, hipMemcpyHostToDevice);
+        hipError_t e = hipMalloc(&weight->d_data, sr::linear_weight_bytes(rows, cols, dtype));
+        if (dtype == SAFETYRAISE_KERNEL_DTYPE_BF16) {
+            // the row-major bytes go through a temporary device buffer into
+            // the tile layout the bf16 kernels read
+            void *rowmajor = nullptr;
+            if (e == hipSuccess) e = hipMalloc(&rowmajor, bytes);
+            if (e == hipSuccess) e = hipMemcpy(rowmajor, data, bytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) {
+                e = sr::linear_pack_bf16(context->stream, rowmajor, weight->d_data, rows, cols);
+            }
+            if (e == hipSuccess) e = hipStreamSynchronize(context->stream);
+            if (rowmajor != nullptr) {
+                const hipError_t f = hipFree(rowmajor);
+                if (e == hipSuccess) e = f;
+            }
+        } else if (e == hipSuccess) {
+            e = hipMemcpy(weight->d_data, data, bytes, hipMemcpyHostToDevice);
+        }
         if (e != hipSuccess) {
             if (weight->d_data != nullptr) (void)hipFree(weight->d_data);
             delete weight;

@@ -103,7 +103,8 @@ struct safetyraise_kernel_context {
 };
 
 // A linear weight [rows][cols] in its own dtype (F32, F16 or BF16), on the
-// device for the life of the handle.
+// device for the life of the handle: F32 and F16 row-major, BF16 in the 1 KB
+// tiles of linear_pack_bf16.
 struct safetyraise_kernel_weight {
     uint64_t rows = 0;
     uint64_t cols = 0;
@@ -335,6 +336,12 @@ hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r);
 // (linear_kernels.hip).  scratch holds linear_scratch_bytes(...) bytes of
 // partial sums (none when that is 0) for calls that split K.
 size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus);
+// Device bytes of a [rows][cols] weight as the kernels read it: row-major for
+// F32 and F16, whole 1 KB tiles for BF16 (SIZE_MAX when that overflows).
+size_t linear_weight_bytes(uint64_t rows, uint64_t cols, uint32_t dtype);
+// The BF16 tile layout in dst from a row-major bf16 weight in device memory.
+hipError_t linear_pack_bf16(hipStream_t stream, const void *src, void *dst, uint64_t rows,
+                            uint64_t cols);
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
                          float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
                          int num_cus);

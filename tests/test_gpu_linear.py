@@ -12,7 +12,10 @@ over several workgroups whose partial sums a second kernel adds (shapes
 (1, 4096, 512), (3, 2001, 100), (5, 1030, 20), the 3072-column device call and
 two of the projection shapes do); calls with at least two workgroups per CU
 ((16, 512, 8192), (32, 130, 4100)) keep two k blocks per register set instead
-of four.
+of four.  A bf16 weight is stored in 16 x 32 tiles padded with zeros, so
+shapes whose rows are not a multiple of 16 or columns not a multiple of 32
+((9, 1000, 48): vector loads of x with a part-filled last block; 2001, 1030,
+3 columns: scalar loads of x) read padding that must add nothing.
 """
 import ctypes as C
 
@@ -86,7 +89,8 @@ def test_known_answer_capabilities_and_errors(pkg, backend):
 @pytest.mark.parametrize("dtype", [F32, F16, BF16])
 @pytest.mark.parametrize("rows,cols,out", [(1, 4096, 512), (7, 96, 33), (64, 1001, 257),
                                            (17, 3, 5), (40, 130, 16), (3, 2001, 100),
-                                           (5, 1030, 20), (16, 512, 8192), (32, 130, 4100)])
+                                           (5, 1030, 20), (16, 512, 8192), (32, 130, 4100),
+                                           (9, 1000, 48)])
 def test_random_inputs_match_the_oracle(backend, rng, dtype, rows, cols, out):
     x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
     bits = weight_bits(rng.standard_normal((out, cols)), dtype)
