@@ -51,7 +51,7 @@ def parse():
                             "copy"])
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
-    p.add_argument("--prefill-steps", type=int, default=5)
+    p.add_argument("--prefill-steps", type=int, default=10)
     p.add_argument("--layers", type=int, default=36)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--seed", type=int, default=0x5A5A0001)
@@ -69,17 +69,54 @@ def traffic_from_profiles(kernel_tag: str):
         return None
 
 
-def kernel_pass(backend, run, calls):
+def _load_roctx():
+    """The ROCTx range API: `rocprofv3 --marker-trace` records the ranges, and
+    without a profiler the calls do nothing.  None when the library is absent."""
+    for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1"):
+        try:
+            lib = C.CDLL(name)
+        except OSError:
+            continue
+        lib.roctxRangePushA.argtypes = [C.c_char_p]
+        lib.roctxRangePushA.restype = C.c_int
+        lib.roctxRangePop.restype = C.c_int
+        return lib
+    return None
+
+
+_ROCTX = _load_roctx()
+
+
+def region_begin(name: str) -> None:
+    """Opens a ROCTx range around a bench region (the timed steps or the
+    kernel-timing pass), called with the stream idle: a kernel trace of the
+    run then tells that region's dispatches from the rest."""
+    if _ROCTX is not None:
+        _ROCTX.roctxRangePushA(name.encode())
+
+
+def region_end() -> None:
+    """Closes the range region_begin opened (after a synchronize)."""
+    if _ROCTX is not None:
+        _ROCTX.roctxRangePop()
+
+
+def kernel_pass(backend, run, calls, name):
     """Runs `run()` (which makes `calls` plugin calls) with the plugin's kernel
     timing on: each launch's device duration from the start/stop timestamps of
     its own dispatch (hipExtLaunchKernelGGL events on the plugin's stream), the
-    figure a profiler's kernel trace records.  Returns {kernel name:
-    {"per_call": launches per call, "us": mean duration}}."""
-    backend.timing(True)
+    figure a profiler's kernel trace records.  The pass follows the timed
+    steps directly, with the GPU in the same state; the events stay out of
+    the timed steps, where they would slow the host's launches.  `name`
+    labels the pass's ROCTx range.  Returns {kernel name: {"per_call":
+    launches per call, "us": mean duration}}."""
+    backend.timing(True)  # synchronizes the stream
+    region_begin(f"{name} timing pass")
     try:
         run()
-        times = backend.kernel_times()
+        times = backend.kernel_times()  # synchronizes the stream
     finally:
+        region_end()
         backend.timing(False)
     return {name: {"per_call": round(n / calls, 3), "us": round(us, 2)}
             for name, (n, us) in times.items()}
@@ -166,6 +203,7 @@ def bench_decode(args, torch, pkg):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    region_begin("decode timed")
     t0.record(stream)
     for s in range(args.warmup, total_steps):
         for l in range(layers):
@@ -174,6 +212,7 @@ def bench_decode(args, torch, pkg):
                 backend.check(st, "attention_forward")
     t1.record(stream)
     torch.cuda.synchronize()
+    region_end()
     backend.synchronize()
     total_ms = t0.elapsed_time(t1)
     # kernel durations in a second pass of the same number of steps (the
@@ -187,7 +226,7 @@ def bench_decode(args, torch, pkg):
                 if st != 0:
                     backend.check(st, "attention_forward")
 
-    kernels = kernel_pass(backend, second_pass, args.steps * layers)
+    kernels = kernel_pass(backend, second_pass, args.steps * layers, "decode")
     ms_per_step = total_ms / args.steps
     bytes_total = sum(step_bytes(s) for s in range(args.warmup, total_steps)) * layers
     value = bytes_total / (total_ms * 1e-3) / 1e9
@@ -361,11 +400,13 @@ def bench_prefill(args, torch, pkg, steps, warmup):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    region_begin("prefill timed")
     t0.record(stream)
     for s in range(steps):
         run_step()
     t1.record(stream)
     torch.cuda.synchronize()
+    region_end()
     backend.synchronize()
     total_ms = t0.elapsed_time(t1)
     # kernel durations (the roofline's launch figure) come from a second pass
@@ -377,7 +418,7 @@ def bench_prefill(args, torch, pkg, steps, warmup):
         for s in range(steps):
             run_step()
 
-    kernels = kernel_pass(backend, second_pass, steps * nchunk)
+    kernels = kernel_pass(backend, second_pass, steps * nchunk, "prefill")
     ms_per_step = total_ms / steps
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
     # the attention kernel of the call: the launch route picks it by shape
@@ -537,11 +578,13 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    region_begin("gdn-decode timed")
     t0.record(stream)
     for s in range(steps):
         run(warmup + s)
     t1.record(stream)
     torch.cuda.synchronize()
+    region_end()
     backend.synchronize()
     # kernel durations in a second pass, outside the timed region, after one
     # untimed step
@@ -551,7 +594,7 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
         for s in range(steps):
             run(warmup + steps + 1 + s)
 
-    kernels = kernel_pass(backend, second_pass, steps * layers)
+    kernels = kernel_pass(backend, second_pass, steps * layers, "gdn-decode")
     C_ = 2 * hk * dk + hv * dv
     per_layer = (2 * nseq * hv * dv * dk * 4          # state read + write
                  + 2 * nseq * C_ * (K - 1) * 4        # conv history read + write
@@ -650,10 +693,12 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        region_begin("gdn-prefill timed")
         t0.record(stream)
         run()
         t1.record(stream)
         torch.cuda.synchronize()
+        region_end()
         total_ms += t0.elapsed_time(t1)
     backend.synchronize()
     # kernel durations in a second pass, outside the timed region
@@ -663,7 +708,7 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
             reset()
             run()
 
-    kernels = kernel_pass(backend, second_pass, steps * nchunk)
+    kernels = kernel_pass(backend, second_pass, steps * nchunk, "gdn-prefill")
     ms = total_ms / steps
     flops = 7 * dk * dv * hv * nseq * total
     tflops = flops / (ms * 1e-3) / 1e12
@@ -780,11 +825,13 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    region_begin("linear timed")
     t0.record(stream)
     for _ in range(steps):
         run()
     t1.record(stream)
     torch.cuda.synchronize()
+    region_end()
     backend.synchronize()
     run()
     # kernel durations in a second pass over the same rotation of all seven
@@ -794,7 +841,7 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
     # per wave); timing the two big calls alone would leave 201 MB of weights
     # cached between calls and overstate the HBM rate.
     kernels = kernel_pass(backend, lambda: [run() for _ in range(steps)],
-                          steps * len(LINEAR_SHAPES))
+                          steps * len(LINEAR_SHAPES), "linear")
     per_call = [o * i * 2 + rows * (i + o) * 4 for o, i in LINEAR_SHAPES]
     per_step = sum(per_call)
     ms = t0.elapsed_time(t1) / steps
@@ -902,17 +949,24 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
         for s_ in ids:
             pool.truncate(s_, ctx_len)  # host bookkeeping only
 
+    # each call streams 2.1 GB from HBM: under this load the GPU's clocks
+    # settle within the first ~3 ms (about ten calls, each call about 15 %
+    # slower than the first ones), so the timed steps and the timing pass
+    # both start after at least that much
+    warmup = max(warmup, 10)
     for _ in range(warmup):
         run()
     backend.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    region_begin("verify timed")
     t0.record(stream)
     for s_ in range(steps):
         run()
     t1.record(stream)
     torch.cuda.synchronize()
+    region_end()
     backend.synchronize()
     ms = t0.elapsed_time(t1) / steps
     # kernel durations in a second pass (outside the timed region), after two
@@ -924,7 +978,7 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
         for _ in range(steps):
             run()
 
-    kernels = kernel_pass(backend, second_pass, steps)
+    kernels = kernel_pass(backend, second_pass, steps, "verify")
     call_us = kernels["attn_verify_kernel"]["us"]
     keys = sum(ctx_len + j + 1 for j in range(rows))  # per sequence, summed over rows
     nbytes = nseq * (ctx_len + rows) * kvh * dim * 2 * 2
@@ -1025,10 +1079,10 @@ def main():
         result = bench_decode(args, torch, pkg)
         if not args.no_prefill:
             result["prefill"] = bench_prefill(args, torch, pkg, args.prefill_steps, 2)
-            result["verify"] = bench_verify(args, torch, pkg, 5, 2)
-            result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 10, 3)
-            result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 3, 1)
-            result["linear"] = bench_linear(args, torch, pkg, 10, 3)
+            result["verify"] = bench_verify(args, torch, pkg, 30, 10)
+            result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 20, 3)
+            result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 10, 2)
+            result["linear"] = bench_linear(args, torch, pkg, 50, 5)
     elif args.workload == "verify":
         result = bench_verify(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "MTP verify attention GB/s", "n_gpus": 1, "higher_is_better": True,
