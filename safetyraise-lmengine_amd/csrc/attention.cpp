@@ -125,9 +125,6 @@ int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args
         A.kv_heads != pool->kv_heads || A.head_dim != pool->head_dim) {
         return fail(ctx, kInvalid, "attention head mapping or cache geometry is invalid");
     }
-    if (A.heads / A.kv_heads > 8) {
-        return fail(ctx, kInvalid, "more than 8 query heads per KV head is not supported");
-    }
     // apply_rope shape (math.rs:58-65)
     if (A.rotary_dim == 0 || A.rotary_dim > A.head_dim || A.rotary_dim % 2 != 0) {
         return fail(ctx, kInvalid, "RoPE input shape is invalid");
@@ -184,6 +181,14 @@ int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args
     L.flags = flags;
     L.heads = A.heads;
     L.kv_heads = A.kv_heads;
+    // The kernels take up to 8 query heads per KV head.  A larger group G
+    // runs as kv_rep groups of G / kv_rep heads (the fewest that fit): query
+    // heads are numbered KV head by KV head, so group j of cache head c holds
+    // heads (c kv_rep + j) G / kv_rep onwards and reads c's cache, the KV
+    // head h / G that math.rs:127 gives query head h.
+    const uint32_t group = A.heads / A.kv_heads;
+    L.kv_rep = 1;
+    while (group / L.kv_rep > 8 || group % L.kv_rep != 0) ++L.kv_rep;
     L.head_dim = A.head_dim;
     L.rotary_dim = A.rotary_dim;
     L.eps = A.eps;

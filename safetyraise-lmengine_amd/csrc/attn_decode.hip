@@ -62,7 +62,9 @@ struct DecodeParams {
     uint32_t page_tokens;
     uint32_t flags;
     uint32_t heads;
-    uint32_t kv_heads;
+    uint32_t kv_heads;  // KV heads as the grid sees them: the cache's times kv_rep
+    uint32_t kv_rep;    // query-head groups per cache KV head (groups of more
+                        // than 8 heads run as kv_rep groups of heads/kv_heads)
     uint32_t rotary_dim;
     uint32_t mrope[3];
     float eps;
@@ -167,7 +169,9 @@ __device__ void decode_segment(const DecodeParams &p, DecodeShared<D, G> &sh, in
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
     const uint32_t hs = gated ? 2 * D : D;  // q elements per head
     const size_t q_row = (size_t)row * p.heads * hs;
-    const size_t kv_row = ((size_t)row * p.kv_heads + kvh) * D;
+    // the cache's KV head of this (virtual) one, and the cache's head count
+    const uint32_t kvp = kvh / p.kv_rep;
+    const size_t kv_row = ((size_t)row * (p.kv_heads / p.kv_rep) + kvp) * D;
     const uint32_t PT = p.page_tokens;
     const int32_t *table = p.page_table + (size_t)slot * p.pages_per_seq;
 
@@ -200,7 +204,7 @@ __device__ void decode_segment(const DecodeParams &p, DecodeShared<D, G> &sh, in
             const uint32_t tb = cc * kChunk;
             const uint32_t pg = min(tb >> lpt, pg1) - pg0;
             const size_t r =
-                (((size_t)kvh * p.num_pages + sh.pages[pg]) << lpt) + (tb & ((1u << lpt) - 1));
+                (((size_t)kvp * p.num_pages + sh.pages[pg]) << lpt) + (tb & ((1u << lpt) - 1));
             const uint16_t *kp = p.k_pages + r * D + group * D + l16 * DPL;
             const uint16_t *vp = p.v_pages + r * D + group * D + l16 * DPL;
 #pragma unroll
@@ -213,7 +217,7 @@ __device__ void decode_segment(const DecodeParams &p, DecodeShared<D, G> &sh, in
             for (int ps = 0; ps < 4; ++ps) {
                 const uint32_t tok = cc * kChunk + ps * 16 + group;
                 const uint32_t pg = min(tok >> lpt, pg1) - pg0;
-                const size_t r = (((size_t)kvh * p.num_pages + sh.pages[pg]) << lpt) +
+                const size_t r = (((size_t)kvp * p.num_pages + sh.pages[pg]) << lpt) +
                                  (tok & ((1u << lpt) - 1));
                 kb[ps] = load_frag<DPL>(p.k_pages + r * D + l16 * DPL);
                 vb[ps] = load_frag<DPL>(p.v_pages + r * D + l16 * DPL);
@@ -290,11 +294,13 @@ __device__ void decode_segment(const DecodeParams &p, DecodeShared<D, G> &sh, in
     __syncthreads();
 
     // 3. append the new token's k and v (bf16, round to nearest even); it is
-    //    the last token of the sequence, so only this segment reads it
+    //    the last token of the sequence, so only this segment reads it.  The
+    //    kv_rep groups that share a cache head each write it (the same bits,
+    //    computed from the same inputs), so each reads back its own write.
     if (owns_new) {
         const uint32_t tok = ctx;
         const int32_t page = table[tok / PT];
-        const size_t base = (((size_t)kvh * p.num_pages + page) * PT + tok % PT) * D;
+        const size_t base = (((size_t)kvp * p.num_pages + page) * PT + tok % PT) * D;
         if (tid < D) {
             const float kk = sh.vec[G][tid];
             if (!isfinite(kk) || !isfinite(v_new)) {
@@ -806,7 +812,8 @@ hipError_t launch_attn_decode(hipStream_t stream, const AttnLaunch &a, const Seq
     prm.page_tokens = a.pool->page_tokens;
     prm.flags = a.flags;
     prm.heads = a.heads;
-    prm.kv_heads = a.kv_heads;
+    prm.kv_heads = a.kv_heads * a.kv_rep;
+    prm.kv_rep = a.kv_rep;
     prm.rotary_dim = a.rotary_dim;
     prm.mrope[0] = a.mrope[0];
     prm.mrope[1] = a.mrope[1];
@@ -829,7 +836,7 @@ hipError_t launch_attn_decode(hipStream_t stream, const AttnLaunch &a, const Seq
         return hipErrorInvalidValue;  // the host splits packs below this
     }
     prm.total_tokens = (uint32_t)total;
-    const uint32_t g = a.heads / a.kv_heads;
+    const uint32_t g = a.heads / prm.kv_heads;
     switch (a.head_dim) {
         case 64: return launch_d<64>(stream, prm, in, g);
         case 128: return launch_d<128>(stream, prm, in, g);

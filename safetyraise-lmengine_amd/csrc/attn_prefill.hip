@@ -84,7 +84,10 @@ struct PrefillParams {
     uint32_t log2_page_tokens;
     uint32_t flags;
     uint32_t heads;
-    uint32_t kv_heads;
+    uint32_t kv_heads;        // KV heads as the attention grids see them: the cache's times kv_rep
+    uint32_t kv_rep;          // query-head groups per cache KV head (groups of more
+                              // than 8 heads run as kv_rep groups of heads/kv_heads)
+    uint32_t cache_kv_heads;  // the cache's KV heads (the append kernel's)
     uint32_t rotary_dim;
     uint32_t mrope[3];
     float eps;
@@ -225,7 +228,7 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     uint64_t bk = (uint64_t)p.k, bv = (uint64_t)p.v, bkn = (uint64_t)p.k_norm,
              bpt = (uint64_t)p.page_table, bpos = (uint64_t)p.positions, bcs = (uint64_t)p.rope_cs,
              berr = (uint64_t)p.err_word, bkp = (uint64_t)p.k_pages, bvp = (uint64_t)p.v_pages;
-    uint32_t kv_heads = p.kv_heads, flags = p.flags, pages_per_seq = p.pages_per_seq,
+    uint32_t kv_heads = p.cache_kv_heads, flags = p.flags, pages_per_seq = p.pages_per_seq,
              lpt = p.log2_page_tokens, rotary_dim = p.rotary_dim, num_pages = p.num_pages;
     float eps = p.eps;
     asm volatile("" : "+s"(bk), "+s"(bv), "+s"(bkn), "+s"(bpt), "+s"(bpos), "+s"(bcs), "+s"(berr),
@@ -361,7 +364,7 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
 // One call's append: (rows x head quads) waves, four per workgroup.
 template <int D>
 void launch_append(hipStream_t stream, const PrefillParams &p, uint32_t max_rows) {
-    const uint32_t quads = (p.kv_heads + kAppendHeadsPerWave - 1) / kAppendHeadsPerWave;
+    const uint32_t quads = (p.cache_kv_heads + kAppendHeadsPerWave - 1) / kAppendHeadsPerWave;
     const uint32_t waves = max_rows * quads;
     const dim3 grid((waves + 3) / 4, p.nseq);
     if (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) {
@@ -450,7 +453,7 @@ struct TileIo {
         v_pages = p.v_pages;
         table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
         table_first = 0;
-        head_base = (size_t)b.kvh * p.num_pages;
+        head_base = (size_t)(b.kvh / p.kv_rep) * p.num_pages;  // the cache's head
         lpt = p.log2_page_tokens;
         pt_mask = (1u << lpt) - 1;
         n_keys = b.n_keys;
@@ -586,7 +589,7 @@ struct LeanIo {
         k_pages = p.k_pages;
         v_pages = p.v_pages;
         table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
-        head_base = (size_t)b.kvh * p.num_pages;
+        head_base = (size_t)(b.kvh / p.kv_rep) * p.num_pages;  // the cache's head
         lpt = p.log2_page_tokens;
         pt_mask = (1u << lpt) - 1;
         n_keys = b.n_keys;
@@ -1709,7 +1712,7 @@ attn_verify_kernel(const VerifyParams vp) {
         io.lpt = p.log2_page_tokens;
         io.pt_mask = (1u << io.lpt) - 1;
         io.page_bytes = (D * 2) << io.lpt;
-        const size_t head_bytes = (size_t)kvh * p.num_pages * io.page_bytes;
+        const size_t head_bytes = (size_t)(kvh / p.kv_rep) * p.num_pages * io.page_bytes;
         io.k_head = (const unsigned char *)p.k_pages + head_bytes;
         io.v_head = (const unsigned char *)p.v_pages + head_bytes;
         io.last_tok = total - 1;
@@ -1972,7 +1975,9 @@ PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
     p.log2_page_tokens = (uint32_t)__builtin_ctz(pool->page_tokens);
     p.flags = a.flags;
     p.heads = a.heads;
-    p.kv_heads = a.kv_heads;
+    p.kv_heads = a.kv_heads * a.kv_rep;
+    p.kv_rep = a.kv_rep;
+    p.cache_kv_heads = a.kv_heads;
     p.rotary_dim = a.rotary_dim;
     p.mrope[0] = a.mrope[0];
     p.mrope[1] = a.mrope[1];
@@ -1991,7 +1996,7 @@ PrefillParams fill_params(const AttnLaunch &a, int nseq, void *rope_scratch) {
 }  // namespace
 
 bool prefill_supported(const AttnLaunch &a) {
-    const uint32_t g = a.heads / a.kv_heads;
+    const uint32_t g = a.heads / (a.kv_heads * a.kv_rep);
     return (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) && g >= 1 && g <= 8 &&
            a.rotary_dim >= 32 && a.rotary_dim % 32 == 0;
 }
@@ -2005,7 +2010,7 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
     if (nseq <= 0 || nseq > kMetaPerLaunch || !prefill_supported(a) || rope_scratch == nullptr) {
         return hipErrorInvalidValue;
     }
-    const uint32_t g = a.heads / a.kv_heads;
+    const uint32_t g = a.heads / (a.kv_heads * a.kv_rep);
     PrefillParams p = fill_params(a, nseq, rope_scratch);
     switch (a.head_dim) {
         case 64: return launch_d<64>(stream, p, g, seqs, nseq);
@@ -2017,13 +2022,14 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
 
 bool verify_supported(const AttnLaunch &a, uint32_t rows) {
     return prefill_supported(a) && a.head_dim <= 128 && rows >= 2 &&
-           rows * (a.heads / a.kv_heads) <= 64;
+           rows * (a.heads / (a.kv_heads * a.kv_rep)) <= 64;
 }
 
 hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
                               int nseq, void *rope_scratch, const DecodePlanInput &in) {
     if (nseq <= 0 || nseq > kMetaPerLaunch || rope_scratch == nullptr) return hipErrorInvalidValue;
-    const uint32_t g = a.heads / a.kv_heads;
+    const uint32_t kvv = a.kv_heads * a.kv_rep;  // KV heads of the grid
+    const uint32_t g = a.heads / kvv;
     VerifyParams vp{};
     vp.p = fill_params(a, nseq, rope_scratch);
     PrefillParams &p = vp.p;
@@ -2038,7 +2044,7 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         rows_g = std::max(rows_g, seqs[i].rows * g);
     }
     const uint64_t target = (uint64_t)std::max(in.num_cus, 1);
-    uint64_t part = (keys * a.kv_heads + target - 1) / target;
+    uint64_t part = (keys * kvv + target - 1) / target;
     part = std::max<uint64_t>(256, (part + kKeyTile - 1) / kKeyTile * kKeyTile);
     // a partition starting mid-page touches at most part/page_tokens + 2 pages
     const uint64_t max_part =
@@ -2069,7 +2075,7 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
     else launch_append<128>(stream, p, max_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t grid = blocks * a.kv_heads;
+    const uint32_t grid = blocks * kvv;
     if (a.head_dim == 64) return launch_verify_d<64>(stream, vp, grid, waves);
     return launch_verify_d<128>(stream, vp, grid, waves);
 }

@@ -236,6 +236,10 @@ struct AttnLaunch {
     const safetyraise_kernel_kv_pool *pool;
     uint32_t flags;
     uint32_t heads, kv_heads, head_dim, rotary_dim;
+    // query-head groups per cache KV head: a GQA group of G > 8 heads runs
+    // as kv_rep groups of G / kv_rep (the kernels' grids see kv_heads *
+    // kv_rep KV heads, group g reading cache head g / kv_rep)
+    uint32_t kv_rep = 1;
     float eps;
     uint32_t mrope[3];
     const void *q, *k, *v;

@@ -114,6 +114,29 @@ def test_mixed_batch_prefill_decode_and_verify_rows(pkg, backend, rng):
     pool.destroy()
 
 
+@pytest.mark.parametrize("heads,kv_heads,dim,page", [(32, 2, 128, 16), (24, 2, 128, 64),
+                                                     (18, 2, 128, 64), (22, 2, 64, 16),
+                                                     (64, 4, 128, 64)])
+def test_gqa_groups_larger_than_8(pkg, backend, rng, heads, kv_heads, dim, page):
+    # math.rs:109-127 takes any heads that kv_heads divides: query head h
+    # reads KV head h / (heads / kv_heads).  Groups of G = 16, 12, 9, 11 and
+    # 16 query heads (64 / 4, the Qwen3-235B shape) run as groups of at most
+    # 8 sharing one cache head; one call holds a prefill chunk, a decode row
+    # and a verify block (3 rows), each against the oracle.
+    pool = new_pool(pkg, backend, kv_heads, dim, page_tokens=page, max_tokens=1024, seqs=5)
+    gq, gk = gammas(rng, dim)
+    cases = [Case(rng, pool, heads, kv_heads, dim, ctx=150, rows=40),
+             Case(rng, pool, heads, kv_heads, dim, ctx=333, rows=1),
+             Case(rng, pool, heads, kv_heads, dim, ctx=97, rows=3)]
+    run_case(pkg, backend, pool, cases, rotary=dim, gq=gq, gk=gk)
+    # decode and 2-row verify calls of their own (no prefill row in the call,
+    # so their page-table entries travel in the append kernel's arguments)
+    more = [Case(rng, pool, heads, kv_heads, dim, ctx=500, rows=1),
+            Case(rng, pool, heads, kv_heads, dim, ctx=64, rows=2)]
+    run_case(pkg, backend, pool, more, rotary=dim, gq=gq, gk=gk)
+    pool.destroy()
+
+
 def test_prefill_whole_equals_chunked_then_decode(pkg, backend, rng):
     # invariants (native.rs:431-455): one 96-row call == chunks of 32 + 64,
     # and a decode row after either matches the oracle
