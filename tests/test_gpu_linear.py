@@ -133,6 +133,24 @@ def test_projection_shapes_integer_inputs_bit_exact(backend, rng, rows, cols, ou
         prepared.destroy()
 
 
+@pytest.mark.parametrize("rows,cols,out", [(7, 1000, 12010), (9, 12000, 4096)])
+def test_multi_tile_plans_with_partial_blocks(backend, rng, rows, cols, out):
+    # the plans with 3 (12010 outputs, last workgroup's tiles partly past N)
+    # and 4 output tiles per wave (4096 outputs, K split over 4 workgroups),
+    # with K not a multiple of 32: the waves' ranges end inside a block, so
+    # the masked path reads the zero-padded last block of every tile
+    x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((out, cols)), BF16)
+    got = backend.linear(bits, x, BF16)
+    ref = O.linear(x, bits, BF16)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, BF16)).T
+    bad = np.abs(got - ref) > 1e-5 * mag + 1e-4 * np.abs(ref)
+    assert not bad.any(), (rows, cols, out, np.abs(got - ref).max())
+    xi = rng.integers(-8, 9, size=(rows, cols)).astype(np.float32)
+    wi = weight_bits(rng.integers(-8, 9, size=(out, cols)).astype(np.float32), BF16)
+    assert np.array_equal(backend.linear(wi, xi, BF16), O.linear(xi, wi, BF16))
+
+
 @pytest.mark.parametrize("cols", [256, 3072])  # 3072: K split over workgroups
 def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod, cols):
     torch = torch_mod
