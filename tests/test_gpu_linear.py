@@ -151,6 +151,21 @@ def test_multi_tile_plans_with_partial_blocks(backend, rng, rows, cols, out):
     assert np.array_equal(backend.linear(wi, xi, BF16), O.linear(xi, wi, BF16))
 
 
+@pytest.mark.parametrize("dtype", [F32, F16])
+def test_row_major_weights_on_the_three_tile_plan(backend, rng, dtype):
+    # 12288 outputs take the 3-tiles-per-wave plan for f32 and f16 weights
+    # too (row-major, widened to f32 on the f32 MFMA); K = 2056 leaves the
+    # waves' ranges ending inside a block
+    rows, cols, out = 6, 2056, 12288
+    x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((out, cols)), dtype)
+    got = backend.linear(bits, x, dtype)
+    ref = O.linear(x, bits, dtype)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, dtype)).T
+    bad = np.abs(got - ref) > 1e-5 * mag + 1e-4 * np.abs(ref)
+    assert not bad.any(), (dtype, np.abs(got - ref).max())
+
+
 @pytest.mark.parametrize("cols", [256, 3072])  # 3072: K split over workgroups
 def test_device_pointer_entry_matches_host_entry(backend, rng, torch_mod, cols):
     torch = torch_mod
