@@ -11,7 +11,7 @@
 // of 8 at a quarter of the rate.
 //
 // Weight layout.  F32 and F16 weights stay row-major as given.  A BF16 weight
-// is repacked once, when its handle is created (linear_pack_weight), into
+// is repacked once, when its handle is created (linear_pack_bf16), into
 // 1 KB tiles: for output tile t (16 rows) and k block b (32 columns) the 512
 // elements from (t * nblk + b) * 512 on hold, at 8 (16 g + r), W[16 t + r]
 // [32 b + 8 g .. + 8], with zeros past N and K.  Lane (r, g) then loads its
@@ -319,6 +319,169 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
     y[i] = s;
 }
 
+// ---------------------------------------------------------------------------
+// Calls with many rows (prefill chunks) on bf16 weights: a tiled product.
+// A workgroup owns 128 rows x 128 outputs; its 8 waves are 4 (rows) x 2
+// (outputs), each computing 32 rows x 64 outputs (2 x 4 tiles of 16 x 16).
+// Per stage of 64 k (two 32-k blocks) the workgroup loads the 128 x 64 f32
+// x tile once, splits it (split3) and stores the three bf16 parts to LDS in
+// MFMA lane order, double-buffered; a wave reads its row tiles' parts with
+// ds_read_b128 and its 4 weight tiles straight from the tile layout (16
+// bytes per lane, prefetched one stage ahead).  So x is split once per
+// workgroup and read from HBM once per 128 outputs, the weight once per 128
+// rows.  Two accumulation chains per tile: the hi part's products, and the
+// mid and lo parts' (three chains of 8 tiles would not fit the registers of
+// two waves per SIMD).  Requires K % 64 == 0 and a 16-byte aligned x (the
+// host checks); rows past M and tiles past N read clamped copies whose
+// results are not stored.
+// ---------------------------------------------------------------------------
+constexpr int kGemmWM = 4, kGemmWN = 2;  // waves over rows, over outputs
+constexpr int kGemmRT = 2, kGemmCT = 4;  // 16 x 16 tiles per wave: rows, outputs
+constexpr int kGemmBM = 16 * kGemmRT * kGemmWM;  // 128 rows per workgroup
+constexpr int kGemmBN = 16 * kGemmCT * kGemmWN;  // 128 outputs per workgroup
+constexpr int kGemmKB = 2;                       // 32-k blocks per stage
+constexpr uint32_t kGemmK = kGemmKB * kLinBlock;  // 64 k per stage
+constexpr uint32_t kGemmMinRows = 64;             // rows from which calls take this kernel
+// one stage of split x in LDS: [k block][part][row tile][lane] x 16 bytes
+constexpr int kGemmStageBytes = kGemmKB * 3 * (kGemmBM / 16) * 64 * 16;
+
+__global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const void *w, float *y,
+                                                         uint32_t M, uint32_t N, uint32_t K) {
+    extern __shared__ __align__(16) unsigned char gemm_lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave % kGemmWM, wn = wave / kGemmWM;
+    const uint32_t m0 = blockIdx.y * kGemmBM, n0 = blockIdx.x * kGemmBN;
+    const uint32_t nblk = K / kLinBlock;
+    const uint32_t stages = K / kGemmK;
+    const uint32_t last_tile = (N - 1) / kLinTile;
+
+    // x chunks this thread loads per stage: c = tid and tid + 512 of the
+    // stage's 1024 (row tile, k block, lane) chunks of 8 values
+    size_t xoff[2];
+    uint32_t lds_chunk[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint32_t c = (uint32_t)tid + 512u * u;
+        const uint32_t rt = c / 128, kb = (c / 64) % 2, l = c % 64;
+        const uint32_t row = min(m0 + 16 * rt + (l & 15), M - 1);
+        xoff[u] = (size_t)row * K + kLinBlock * kb + 8 * (l >> 4);
+        lds_chunk[u] = (kb * 3 * (kGemmBM / 16) + rt) * 64 + l;  // part 0; parts add (BM/16) 64
+    }
+    // this wave's weight tiles: 16 bytes of block 0 per lane (tiles past N
+    // read the last one)
+    const uint16_t *wt[kGemmCT];
+#pragma unroll
+    for (int j = 0; j < kGemmCT; ++j) {
+        const uint32_t tile = min(n0 / kLinTile + kGemmCT * wn + j, last_tile);
+        wt[j] = (const uint16_t *)w + (size_t)tile * nblk * 512 + (size_t)lane * 8;
+    }
+    typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
+    auto lds_at = [&](uint32_t stage_buf, uint32_t chunk) {
+        return (u32x4g *)(gemm_lds + (size_t)stage_buf * kGemmStageBytes) + chunk;
+    };
+    auto load_x = [&](uint32_t s, f32x8 (&xv)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) xv[u] = load8_at<SAFETYRAISE_KERNEL_DTYPE_F32>(x, xoff[u] + (size_t)kGemmK * s);
+    };
+    auto store_x = [&](uint32_t buf, const f32x8 (&xv)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            bf16x8 part[3];
+            split3(xv[u], part[0], part[1], part[2]);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                *lds_at(buf, lds_chunk[u] + (uint32_t)c * (kGemmBM / 16) * 64) =
+                    __builtin_bit_cast(u32x4g, part[c]);
+            }
+        }
+    };
+    auto load_w = [&](uint32_t s, bf16x8 (&wv)[kGemmKB][kGemmCT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kb = 0; kb < kGemmKB; ++kb)
+#pragma unroll
+            for (int j = 0; j < kGemmCT; ++j)
+                wv[kb][j] = *(const bf16x8 *)(wt[j] + (size_t)(kGemmKB * s + kb) * 512);
+    };
+
+    f32x4 acc[kGemmRT][kGemmCT][2];
+#pragma unroll
+    for (int i = 0; i < kGemmRT; ++i)
+#pragma unroll
+        for (int j = 0; j < kGemmCT; ++j)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[i][j][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    f32x8 xv[2];
+    bf16x8 wa[kGemmKB][kGemmCT], wb[kGemmKB][kGemmCT];
+    load_x(0, xv);
+    load_w(0, wa);
+    store_x(0, xv);
+    __syncthreads();
+    auto compute = [&](uint32_t buf, const bf16x8 (&wv)[kGemmKB][kGemmCT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kb = 0; kb < kGemmKB; ++kb) {
+            bf16x8 a[kGemmRT][3];
+#pragma unroll
+            for (int i = 0; i < kGemmRT; ++i)
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    const uint32_t chunk = ((kb * 3 + c) * (kGemmBM / 16) + kGemmRT * wm + i) * 64 + lane;
+                    a[i][c] = __builtin_bit_cast(bf16x8, *lds_at(buf, chunk));
+                }
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+#pragma unroll
+                for (int i = 0; i < kGemmRT; ++i)
+#pragma unroll
+                    for (int j = 0; j < kGemmCT; ++j) {
+                        f32x4 &ac = acc[i][j][c == 0 ? 0 : 1];
+                        ac = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][c], wv[kb][j], ac, 0, 0, 0);
+                    }
+        }
+    };
+    // stages in pairs, so that the two weight register sets alternate by name
+    uint32_t s = 0;
+    for (; s + 2 <= stages; s += 2) {
+        // stage s (weights in wa), loading stage s + 1
+        const bool more1 = s + 1 < stages;
+        if (more1) {
+            load_x(s + 1, xv);
+            load_w(s + 1, wb);
+        }
+        compute(s & 1, wa);
+        if (more1) store_x((s + 1) & 1, xv);
+        __syncthreads();
+        // stage s + 1 (weights in wb), loading stage s + 2
+        const bool more2 = s + 2 < stages;
+        if (more2) {
+            load_x(s + 2, xv);
+            load_w(s + 2, wa);
+        }
+        compute((s + 1) & 1, wb);
+        if (more2) store_x((s + 2) & 1, xv);
+        __syncthreads();
+    }
+    if (s < stages) compute(s & 1, wa);
+
+    // the mid + lo chain, then hi; lane (r, g) holds y[row 4g + e][output
+    // r] of each tile in element e
+    const uint32_t r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < kGemmRT; ++i)
+#pragma unroll
+        for (int j = 0; j < kGemmCT; ++j) {
+            const f32x4 sum = acc[i][j][1] + acc[i][j][0];
+            const uint32_t n = n0 + kLinTile * (kGemmCT * wn + j) + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + kLinTile * (kGemmRT * wm + i) + 4 * g + e;
+                if (m < M && n < N) y[(size_t)m * N + n] = sum[e];
+            }
+        }
+}
+
 // The bf16 tile layout from a row-major [N][K] weight: thread c writes the
 // 16 bytes lane c % 64 loads from tile block c / 64 (blocks in tile-major
 // order, nblk per tile), zeros past N and K.
@@ -483,6 +646,22 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
+    }
+    // the tiled product when its 128 x 128 tiles give at least half the CUs
+    // a workgroup (fewer, and the row-tile kernel's weight stream is faster)
+    const uint64_t gemm_tiles =
+        (uint64_t)((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN);
+    if (dtype == SAFETYRAISE_KERNEL_DTYPE_BF16 && M >= kGemmMinRows && K % kGemmK == 0 &&
+        ((uintptr_t)x & 15u) == 0 && 2 * gemm_tiles >= (uint64_t)(num_cus > 0 ? num_cus : 1)) {
+        // the two x stages take 96 KB of LDS, above the default limit
+        static const hipError_t configured = hipFuncSetAttribute(
+            (const void *)linear_gemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+            2 * kGemmStageBytes);
+        if (configured != hipSuccess) return configured;
+        const dim3 grid((N + kGemmBN - 1) / kGemmBN, (M + kGemmBM - 1) / kGemmBM);
+        SR_LAUNCH("linear_gemm_kernel", linear_gemm_kernel, grid, dim3(64 * kGemmWM * kGemmWN),
+                  2 * kGemmStageBytes, stream, x, w, y, M, N, K);
+        return hipGetLastError();
     }
     const LinPlan plan = linear_plan(M, N, K, dtype, num_cus);
     const uint32_t splits = plan.splits;

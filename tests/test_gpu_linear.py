@@ -151,6 +151,34 @@ def test_multi_tile_plans_with_partial_blocks(backend, rng, rows, cols, out):
     assert np.array_equal(backend.linear(wi, xi, BF16), O.linear(xi, wi, BF16))
 
 
+@pytest.mark.parametrize("rows,cols,out", [(256, 64, 8192), (130, 512, 16000), (300, 192, 6000)])
+def test_prefill_sized_calls_take_the_tiled_product(backend, rng, rows, cols, out):
+    # 64+ rows with K a multiple of 64 on a bf16 weight, with at least 128
+    # output tiles of 128 x 128, take the tiled product (x split once per
+    # workgroup through LDS): one 64-k stage, an even and an odd number of
+    # stages, rows and outputs past the last whole tile
+    x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
+    bits = weight_bits(rng.standard_normal((out, cols)), BF16)
+    got = backend.linear(bits, x, BF16)
+    ref = O.linear(x, bits, BF16)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, BF16)).T
+    bad = np.abs(got - ref) > 1e-5 * mag + 1e-4 * np.abs(ref)
+    assert not bad.any(), (rows, cols, out, np.abs(got - ref).max())
+
+
+def test_prefill_sized_integer_inputs_bit_exact(backend, rng):
+    x = rng.integers(-8, 9, size=(256, 128)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(8200, 128)).astype(np.float32)
+    bits = weight_bits(w, BF16)
+    prepared = backend.create_weight(bits, BF16)
+    try:
+        assert np.array_equal(backend.linear(prepared, x), O.linear(x, bits, BF16))
+        x2 = x[::-1].copy()  # a second call on the same weight
+        assert np.array_equal(backend.linear(prepared, x2), O.linear(x2, bits, BF16))
+    finally:
+        prepared.destroy()
+
+
 @pytest.mark.parametrize("dtype", [F32, F16])
 def test_row_major_weights_on_the_three_tile_plan(backend, rng, dtype):
     # 12288 outputs take the 3-tiles-per-wave plan for f32 and f16 weights
