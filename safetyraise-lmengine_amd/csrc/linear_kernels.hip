@@ -321,19 +321,22 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
 
 // ---------------------------------------------------------------------------
 // Calls with many rows (prefill chunks) on bf16 weights: a tiled product.
-// A workgroup owns 128 rows x 128 outputs; its 8 waves are 4 (rows) x 2
-// (outputs), each computing 32 rows x 64 outputs (2 x 4 tiles of 16 x 16).
-// Per stage of 64 k (two 32-k blocks) the workgroup loads the 128 x 64 f32
-// x tile once, splits it (split3) and stores the three bf16 parts to LDS in
-// MFMA lane order, double-buffered; a wave reads its row tiles' parts with
-// ds_read_b128 and its 4 weight tiles straight from the tile layout (16
-// bytes per lane, prefetched one stage ahead).  So x is split once per
-// workgroup and read from HBM once per 128 outputs, the weight once per 128
-// rows.  Two accumulation chains per tile: the hi part's products, and the
-// mid and lo parts' (three chains of 8 tiles would not fit the registers of
-// two waves per SIMD).  Requires K % 64 == 0 and a 16-byte aligned x (the
-// host checks); rows past M and tiles past N read clamped copies whose
-// results are not stored.
+// linear_split_x_kernel first writes x once as its three bf16 parts (split3)
+// in MFMA lane order: for row tile t (16 rows), k block b (32 columns) and
+// part c, the 1 KB at ((t * nblk + b) * 3 + c) KB holds, at lane 16 g + r,
+// x[16 t + r][32 b + 8 g .. + 8].  linear_gemm_kernel then owns 128 rows x
+// 128 outputs per workgroup; its 8 waves are 4 (rows) x 2 (outputs), each
+// computing 32 rows x 64 outputs (2 x 4 tiles of 16 x 16).  Per stage of 64 k
+// (two 32-k blocks) the workgroup copies its 48 KB of split x straight from
+// memory into LDS (global_load_lds: no registers, no VALU), double-buffered;
+// a wave reads its row tiles' parts with ds_read_b128 and its 4 weight tiles
+// straight from the tile layout (16 bytes per lane, prefetched one stage
+// ahead).  So x is read once per 128 outputs and the weight once per 128
+// rows, and the loop is loads and MFMAs only.  Two accumulation chains per
+// tile: the hi part's products, and the mid and lo parts' (three chains of 8
+// tiles would not fit the registers of two waves per SIMD).  Requires K % 64
+// == 0; rows past M and tiles past N read clamped copies whose results are
+// not stored.
 // ---------------------------------------------------------------------------
 constexpr int kGemmWM = 4, kGemmWN = 2;  // waves over rows, over outputs
 constexpr int kGemmRT = 2, kGemmCT = 4;  // 16 x 16 tiles per wave: rows, outputs
@@ -344,9 +347,40 @@ constexpr uint32_t kGemmK = kGemmKB * kLinBlock;  // 64 k per stage
 constexpr uint32_t kGemmMinRows = 64;             // rows from which calls take this kernel
 // one stage of split x in LDS: [k block][part][row tile][lane] x 16 bytes
 constexpr int kGemmStageBytes = kGemmKB * 3 * (kGemmBM / 16) * 64 * 16;
+constexpr int kGemmStageBlocks = kGemmStageBytes / 1024;  // 1 KB blocks per stage (48)
 
-__global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const void *w, float *y,
-                                                         uint32_t M, uint32_t N, uint32_t K) {
+// Thread c: lane c % 64 of (row tile, k block) c / 64, its 8 values split.
+template <bool kVec>
+__global__ __launch_bounds__(256) void linear_split_x_kernel(const float *x, uint16_t *xs,
+                                                            uint32_t M, uint32_t K,
+                                                            uint64_t chunks) {
+    const uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const uint32_t nblk = K / kLinBlock;
+    const uint32_t lane = (uint32_t)(c & 63);
+    const uint64_t tb = c >> 6;
+    const uint32_t t = (uint32_t)(tb / nblk), b = (uint32_t)(tb % nblk);
+    const uint32_t row = min(kLinTile * t + (lane & 15), M - 1);
+    const size_t off = (size_t)row * K + kLinBlock * b + 8 * (lane >> 4);
+    f32x8 v;
+    if constexpr (kVec) {
+        v = load8_at<SAFETYRAISE_KERNEL_DTYPE_F32>(x, off);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = x[off + j];
+    }
+    bf16x8 part[3];
+    split3(v, part[0], part[1], part[2]);
+    typedef uint32_t u32x4s __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        *(u32x4s *)(xs + ((tb * 3 + p) * 64 + lane) * 8) = __builtin_bit_cast(u32x4s, part[p]);
+    }
+}
+
+__global__ __launch_bounds__(512) void linear_gemm_kernel(const uint16_t *xs, const void *w,
+                                                         float *y, uint32_t M, uint32_t N,
+                                                         uint32_t K) {
     extern __shared__ __align__(16) unsigned char gemm_lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -356,18 +390,20 @@ __global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const 
     const uint32_t nblk = K / kLinBlock;
     const uint32_t stages = K / kGemmK;
     const uint32_t last_tile = (N - 1) / kLinTile;
+    const uint32_t last_row_tile = (M - 1) / kLinTile;
 
-    // x chunks this thread loads per stage: c = tid and tid + 512 of the
-    // stage's 1024 (row tile, k block, lane) chunks of 8 values
-    size_t xoff[2];
-    uint32_t lds_chunk[2];
+    // the split-x blocks this wave copies per stage: blocks q = 6 wave .. +6
+    // of the stage's 48, block q = (k block, part, row tile) in LDS order
+    const uint16_t *xsrc[kGemmStageBlocks / 8];
+    uint32_t xdst[kGemmStageBlocks / 8];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const uint32_t c = (uint32_t)tid + 512u * u;
-        const uint32_t rt = c / 128, kb = (c / 64) % 2, l = c % 64;
-        const uint32_t row = min(m0 + 16 * rt + (l & 15), M - 1);
-        xoff[u] = (size_t)row * K + kLinBlock * kb + 8 * (l >> 4);
-        lds_chunk[u] = (kb * 3 * (kGemmBM / 16) + rt) * 64 + l;  // part 0; parts add (BM/16) 64
+    for (int i = 0; i < kGemmStageBlocks / 8; ++i) {
+        const uint32_t q = (uint32_t)wave * (kGemmStageBlocks / 8) + i;
+        const uint32_t rt = q % (kGemmBM / 16), part = (q / (kGemmBM / 16)) % 3,
+                       kb = q / (3 * (kGemmBM / 16));
+        const uint32_t t = min(m0 / kLinTile + rt, last_row_tile);
+        xsrc[i] = xs + (((size_t)t * nblk + kb) * 3 + part) * 512 + (size_t)lane * 8;
+        xdst[i] = q * 1024;
     }
     // this wave's weight tiles: 16 bytes of block 0 per lane (tiles past N
     // read the last one)
@@ -378,23 +414,15 @@ __global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const 
         wt[j] = (const uint16_t *)w + (size_t)tile * nblk * 512 + (size_t)lane * 8;
     }
     typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
-    auto lds_at = [&](uint32_t stage_buf, uint32_t chunk) {
-        return (u32x4g *)(gemm_lds + (size_t)stage_buf * kGemmStageBytes) + chunk;
-    };
-    auto load_x = [&](uint32_t s, f32x8 (&xv)[2]) __attribute__((always_inline)) {
+    typedef __attribute__((address_space(3))) unsigned char lds_byte;
+    lds_byte *lds = (lds_byte *)gemm_lds;
+    auto copy_x = [&](uint32_t s, uint32_t buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) xv[u] = load8_at<SAFETYRAISE_KERNEL_DTYPE_F32>(x, xoff[u] + (size_t)kGemmK * s);
-    };
-    auto store_x = [&](uint32_t buf, const f32x8 (&xv)[2]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            bf16x8 part[3];
-            split3(xv[u], part[0], part[1], part[2]);
-#pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                *lds_at(buf, lds_chunk[u] + (uint32_t)c * (kGemmBM / 16) * 64) =
-                    __builtin_bit_cast(u32x4g, part[c]);
-            }
+        for (int i = 0; i < kGemmStageBlocks / 8; ++i) {
+            // a stage's two k blocks: block s of the call's stages is k
+            // blocks 2 s, 2 s + 1, i.e. (2 s) * 3 * 512 elements past block 0
+            __builtin_amdgcn_global_load_lds(xsrc[i] + (size_t)s * kGemmKB * 3 * 512,
+                                             lds + buf * kGemmStageBytes + xdst[i], 16, 0, 0);
         }
     };
     auto load_w = [&](uint32_t s, bf16x8 (&wv)[kGemmKB][kGemmCT]) __attribute__((always_inline)) {
@@ -413,11 +441,9 @@ __global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const 
 #pragma unroll
             for (int c = 0; c < 2; ++c) acc[i][j][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    f32x8 xv[2];
     bf16x8 wa[kGemmKB][kGemmCT], wb[kGemmKB][kGemmCT];
-    load_x(0, xv);
+    copy_x(0, 0);
     load_w(0, wa);
-    store_x(0, xv);
     __syncthreads();
     auto compute = [&](uint32_t buf, const bf16x8 (&wv)[kGemmKB][kGemmCT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -428,7 +454,9 @@ __global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const 
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
                     const uint32_t chunk = ((kb * 3 + c) * (kGemmBM / 16) + kGemmRT * wm + i) * 64 + lane;
-                    a[i][c] = __builtin_bit_cast(bf16x8, *lds_at(buf, chunk));
+                    a[i][c] = __builtin_bit_cast(
+                        bf16x8, *(const __attribute__((address_space(3))) u32x4g *)(
+                                    lds + buf * kGemmStageBytes + chunk * 16));
                 }
 #pragma unroll
             for (int c = 0; c < 3; ++c)
@@ -441,26 +469,24 @@ __global__ __launch_bounds__(512) void linear_gemm_kernel(const float *x, const 
                     }
         }
     };
-    // stages in pairs, so that the two weight register sets alternate by name
+    // stages in pairs, so that the two weight register sets alternate by
+    // name; the copy of stage s + 1 into the other buffer is in flight while
+    // stage s computes, and the barrier after it waits for the copy
     uint32_t s = 0;
     for (; s + 2 <= stages; s += 2) {
-        // stage s (weights in wa), loading stage s + 1
         const bool more1 = s + 1 < stages;
         if (more1) {
-            load_x(s + 1, xv);
+            copy_x(s + 1, (s + 1) & 1);
             load_w(s + 1, wb);
         }
         compute(s & 1, wa);
-        if (more1) store_x((s + 1) & 1, xv);
         __syncthreads();
-        // stage s + 1 (weights in wb), loading stage s + 2
         const bool more2 = s + 2 < stages;
         if (more2) {
-            load_x(s + 2, xv);
+            copy_x(s + 2, s & 1);
             load_w(s + 2, wa);
         }
         compute((s + 1) & 1, wb);
-        if (more2) store_x((s + 2) & 1, xv);
         __syncthreads();
     }
     if (s < stages) compute(s & 1, wa);
@@ -623,7 +649,29 @@ hipError_t linear_pack_bf16(hipStream_t stream, const void *src, void *dst, uint
     return hipGetLastError();
 }
 
+namespace {
+constexpr uint32_t kMaxRows = 65535u * kLinTile;  // grid y limit of one row-tile launch
+
+// Whether a call takes the tiled product: bf16 weight, 64+ rows, K a multiple
+// of 64, and 128 x 128 tiles for at least half the CUs (fewer, and the
+// row-tile kernel's weight stream is faster).  Calls above kMaxRows rows run
+// as row blocks without scratch.
+bool gemm_applies(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
+    if (dtype != SAFETYRAISE_KERNEL_DTYPE_BF16 || M < kGemmMinRows || M > kMaxRows ||
+        K % kGemmK != 0) {
+        return false;
+    }
+    const uint64_t tiles = (uint64_t)((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN);
+    return 2 * tiles >= (uint64_t)(num_cus > 0 ? num_cus : 1);
+}
+// split x of a tiled-product call: whole row tiles x K x 3 bf16 parts
+size_t gemm_split_bytes(uint32_t M, uint32_t K) {
+    return (size_t)((M + kLinTile - 1) / kLinTile) * kLinTile * K * 3 * sizeof(uint16_t);
+}
+}  // namespace
+
 size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
+    if (gemm_applies(M, N, K, dtype, num_cus)) return gemm_split_bytes(M, K);
     const uint32_t s = linear_plan(M, N, K, dtype, num_cus).splits;
     return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
@@ -632,7 +680,6 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
                          float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
                          int num_cus) {
     if (M == 0 || N == 0) return hipSuccess;
-    constexpr uint32_t kMaxRows = 65535u * kLinTile;  // grid y limit of one launch
     if (M > kMaxRows) {
         // equal blocks of rows, one launch each: every block has at least
         // kMaxRows / 2 rows, so enough tiles that none splits K and the
@@ -647,20 +694,26 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
         }
         return hipSuccess;
     }
-    // the tiled product when its 128 x 128 tiles give at least half the CUs
-    // a workgroup (fewer, and the row-tile kernel's weight stream is faster)
-    const uint64_t gemm_tiles =
-        (uint64_t)((M + kGemmBM - 1) / kGemmBM) * ((N + kGemmBN - 1) / kGemmBN);
-    if (dtype == SAFETYRAISE_KERNEL_DTYPE_BF16 && M >= kGemmMinRows && K % kGemmK == 0 &&
-        ((uintptr_t)x & 15u) == 0 && 2 * gemm_tiles >= (uint64_t)(num_cus > 0 ? num_cus : 1)) {
-        // the two x stages take 96 KB of LDS, above the default limit
+    if (scratch != nullptr && gemm_applies(M, N, K, dtype, num_cus)) {
+        // x split once into scratch, then the tiled product; its two x
+        // stages take 96 KB of LDS, above the default limit
         static const hipError_t configured = hipFuncSetAttribute(
             (const void *)linear_gemm_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
             2 * kGemmStageBytes);
         if (configured != hipSuccess) return configured;
+        uint16_t *xs = (uint16_t *)scratch;
+        const uint64_t chunks = (uint64_t)((M + kLinTile - 1) / kLinTile) * (K / kLinBlock) * 64;
+        const dim3 sgrid((uint32_t)((chunks + 255) / 256));
+        if (((uintptr_t)x & 15u) == 0) {
+            SR_LAUNCH("linear_split_x_kernel", linear_split_x_kernel<true>, sgrid, dim3(256), 0,
+                      stream, x, xs, M, K, chunks);
+        } else {
+            SR_LAUNCH("linear_split_x_kernel", linear_split_x_kernel<false>, sgrid, dim3(256), 0,
+                      stream, x, xs, M, K, chunks);
+        }
         const dim3 grid((N + kGemmBN - 1) / kGemmBN, (M + kGemmBM - 1) / kGemmBM);
         SR_LAUNCH("linear_gemm_kernel", linear_gemm_kernel, grid, dim3(64 * kGemmWM * kGemmWN),
-                  2 * kGemmStageBytes, stream, x, w, y, M, N, K);
+                  2 * kGemmStageBytes, stream, xs, w, y, M, N, K);
         return hipGetLastError();
     }
     const LinPlan plan = linear_plan(M, N, K, dtype, num_cus);
