@@ -48,7 +48,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
                    choices=["decode", "prefill", "verify", "gdn-decode", "gdn-prefill", "linear",
-                            "copy"])
+                            "linear-prefill", "copy"])
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
     p.add_argument("--prefill-steps", type=int, default=10)
@@ -874,6 +874,87 @@ def bench_linear(args, torch, pkg, steps, warmup, rows=16):
     return result
 
 
+def bench_linear_prefill(args, torch, pkg, steps, warmup, rows=2048):
+    """ABI v1 linear at a prefill chunk's row count: the seven projections of
+    one Qwen3-8B decoder layer (bf16 weights) for 2048 rows, through the
+    device-pointer entry.  One step = the seven calls.  These calls take the
+    tiled product (x split once into three bf16 parts, then 128 x 128 output
+    tiles on v_mfma_f32_16x16x32_bf16).  `value` counts the f32 product's own
+    FLOPs, 2 rows in out per call; the roofline counts the MFMA work, three
+    bf16 passes per exact product, against the dense bf16 peak."""
+    backend = pkg.NativeBackend.load()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    backend.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5A5A0007)
+    weights, xs, ys = [], [], []
+    for out_f, in_f in LINEAR_SHAPES:
+        w = (torch.randn((out_f, in_f), generator=gen, device="cuda") * 0.02).bfloat16()
+        bits = w.view(torch.int16).cpu().numpy().view(np.uint16)
+        weights.append(backend.create_weight(bits, pkg.DTYPE_BF16))
+        xs.append(torch.randn((rows, in_f), generator=gen, device="cuda"))
+        ys.append(torch.empty((rows, out_f), device="cuda"))
+        del w, bits
+    fn = backend.lib.safetyraise_kernel_linear_device
+    ctx = backend.context
+
+    def run():
+        for i, (out_f, in_f) in enumerate(LINEAR_SHAPES):
+            st = fn(ctx, weights[i].handle, C.c_void_p(xs[i].data_ptr()), rows, in_f,
+                    C.c_void_p(ys[i].data_ptr()), rows, out_f)
+            if st != 0:
+                backend.check(st, "linear_device")
+
+    for _ in range(warmup):
+        run()
+    backend.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    region_begin("linear-prefill timed")
+    t0.record(stream)
+    for _ in range(steps):
+        run()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    region_end()
+    backend.synchronize()
+    kernels = kernel_pass(backend, lambda: [run() for _ in range(steps)],
+                          steps * len(LINEAR_SHAPES), "linear-prefill")
+    ms = t0.elapsed_time(t1) / steps
+    flops = [2 * rows * o * i for o, i in LINEAR_SHAPES]
+    tflops = sum(flops) / (ms * 1e-3) / 1e12
+    gemm_us = kernels["linear_gemm_kernel"]["us"]
+    # the roofline: the gate/up shape, the MFMA work of one call (3 passes)
+    # over the average tiled-kernel launch weighted as the calls' FLOPs are
+    launch_flops = sum(flops) / len(flops)
+    mfma_tf = 3 * launch_flops / (gemm_us * 1e-6) / 1e12
+    result = {
+        "workload": f"Qwen3-8B decoder-layer projections (q/k/v/o/gate/up/down, bf16 weights), "
+                    f"{rows} rows, f32 in/out, device pointers",
+        "value": round(tflops, 2), "unit": "TFLOP/s",
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "dtype": "f32 products, exact (x split in three bf16 parts on v_mfma_f32_16x16x32_bf16)",
+        "roofline": {
+            "bound": "mfma", "achieved": round(mfma_tf, 2), "peak": MFMA_BF16_PEAK_TFS,
+            "unit": "TFLOP/s", "frac": round(mfma_tf / MFMA_BF16_PEAK_TFS, 4),
+            "traffic": None,
+            "kernel": "linear_gemm_kernel (all seven calls; achieved = 3 bf16 MFMA passes per "
+                      "exact product, the calls' mean FLOPs over the mean launch)",
+            "launch_us_mean": round(float(gemm_us), 2),
+            "flops_per_launch": int(3 * launch_flops),
+            "exact_product_tflops_per_launch": round(launch_flops / (gemm_us * 1e-6) / 1e12, 2),
+            "fp32_matrix_peak": MFMA_F32_PEAK_TFS,
+        },
+        "kernels": kernels,
+    }
+    for w in weights:
+        w.destroy()
+    backend.close()
+    return result
+
+
 def cpu_baseline_linear(weight, x_dev, rows):
     """The oracle's linear (the reference CPU plugin's loop, 1 thread) on the q
     projection (4096 x 4096 bf16) for 4 of the rows, as weight GB/s."""
@@ -1083,6 +1164,7 @@ def main():
             result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 20, 3)
             result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 10, 2)
             result["linear"] = bench_linear(args, torch, pkg, 50, 5)
+            result["linear"]["prefill_rows"] = bench_linear_prefill(args, torch, pkg, 3, 1)
     elif args.workload == "verify":
         result = bench_verify(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "MTP verify attention GB/s", "n_gpus": 1, "higher_is_better": True,
@@ -1097,6 +1179,11 @@ def main():
     elif args.workload == "linear":
         result = bench_linear(args, torch, pkg, args.steps, args.warmup)
         result = {"metric": "linear weight-stream GB/s", "n_gpus": 1, "higher_is_better": True,
+                  "scaling": "weak", "vs_baseline": None, "data": "synthetic",
+                  "config": {"workload": result.pop("workload")}, **result}
+    elif args.workload == "linear-prefill":
+        result = bench_linear_prefill(args, torch, pkg, args.steps, args.warmup)
+        result = {"metric": "linear TFLOP/s at 2048 rows", "n_gpus": 1, "higher_is_better": True,
                   "scaling": "weak", "vs_baseline": None, "data": "synthetic",
                   "config": {"workload": result.pop("workload")}, **result}
     elif args.workload == "prefill":
