@@ -494,7 +494,7 @@ def cpu_baseline_prefill(q, k, v, positions, gq, gk, heads, kvh, dim, chunk):
 
 
 MFMA_F32_PEAK_TFS = 157.3  # MI355X dense fp32 matrix
-GDN_KERNEL_CHUNK = 32  # rows per chunk of gdn_chunk_kernel (kCk in gdn_kernels.hip)
+GDN_KERNEL_CHUNK = 32  # rows per chunk of the chunked GDN kernels (kCk in gdn_kernels.hip)
 
 
 def gdn_layer_setup(torch, pkg, backend, gen, hk, hv, dk, dv, K, nseq):
@@ -635,9 +635,12 @@ def bench_gdn_decode(args, torch, pkg, steps, warmup, layers=64):
 
 def bench_gdn_prefill(args, torch, pkg, steps, warmup):
     """BASELINE config 4, prefill: 2 sequences x 2048 tokens in chunks of 64 (32 calls
-    per layer); one step = the whole prefill of one layer from a zero state.  The
-    kernel runs the chunked (WY) form of the delta rule in chunks of 32 rows on f32
-    MFMA.  `value` counts the token-serial work, 7 * Dk * Dv per (row, value head)
+    per layer); one step = the whole prefill of one layer from a zero state.  Two
+    kernels run the chunked (WY) form of the delta rule in chunks of 32 rows on f32
+    MFMA: gdn_chunk_prep_kernel (everything that does not involve the state, for all
+    chunks of a call at once) and gdn_chunk_scan_kernel (the products with the
+    state, chunk after chunk); the roofline's duration is the sum of their mean
+    durations per call.  `value` counts the token-serial work, 7 * Dk * Dv per (row, value head)
     (decay, predict, correct, read), independent of the chunking; the roofline
     counts the chunked form's own FLOPs at its chunk size C = 32:
     4 C^2 Dk + 2/3 C^3 + 4 C^2 Dv + 8 C Dk Dv + 2 C^2 Dv per (sequence, value head,
@@ -719,7 +722,7 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
     ck = GDN_KERNEL_CHUNK
     chunked_form = ((4 * ck * ck * dk + 2 * ck ** 3 / 3 + 4 * ck * ck * dv + 8 * ck * dk * dv
                      + 2 * ck * ck * dv) * nseq * hv * (total // ck))
-    chunk_us = kernels["gdn_chunk_kernel"]["us"]
+    chunk_us = kernels["gdn_chunk_prep_kernel"]["us"] + kernels["gdn_chunk_scan_kernel"]["us"]
     chunk_tf = chunked_form / nchunk / (chunk_us * 1e-6) / 1e12
     serial_tf = flops / nchunk / (chunk_us * 1e-6) / 1e12
     result = {
@@ -735,7 +738,8 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
             "unit": "TFLOP/s", "frac": round(chunk_tf / MFMA_F32_PEAK_TFS, 4),
             "frac_token_serial": round(serial_tf / MFMA_F32_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("gdn_prefill_qwen35"),
-            "kernel": "gdn_chunk_kernel<ConvK<4>>",
+            "kernel": "gdn_chunk_prep_kernel<ConvK<4>> + gdn_chunk_scan_kernel (the call's "
+                      "chunked form: sum of the two kernels' mean durations)",
             "launch_us_mean": round(float(chunk_us), 2),
             "flops_per_launch": int(chunked_form / nchunk),
             "flops_per_step": int(chunked_form),

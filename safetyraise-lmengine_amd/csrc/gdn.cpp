@@ -320,10 +320,17 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
         out_off = need;
         need += align_up(out_b);
     }
+    // per-chunk records of the chunked prefill form (host inputs are staged
+    // at 256-byte offsets, so only device qkv can be unaligned)
+    const size_t rec_b = gdn_chunk_rec_bytes(pool, seqs.data(), (int)A.num_seqs, keep,
+                                             !device || ((uintptr_t)A.qkv & 15) == 0);
+    const size_t rec_off = need;
+    need += align_up(rec_b);
     int32_t st = ensure_buffer(ctx, ctx->staging, need, false);
     if (st != kOk) return st;
     char *base = (char *)ctx->staging.ptr;
     g.raw = (float *)base;
+    g.chunk_rec = rec_b > 0 ? (float *)(base + rec_off) : nullptr;
     if (!device) {
         for (auto &r : regions) {
             SR_HIP(ctx, hipMemcpyAsync(base + r.off, r.host, r.bytes, hipMemcpyHostToDevice,

@@ -36,6 +36,7 @@ struct GdnMeta {
     uint32_t parity;     // history buffer holding the current history
     uint32_t state_in;   // state buffer read (index in units of one state)
     uint32_t state_out;  // state buffer written (== state_in but for KEEP_ROWS calls)
+    uint32_t chunk0;     // chunked prefill: the sequence's first chunk record in the launch
 };
 
 struct GdnParams {
@@ -48,6 +49,9 @@ struct GdnParams {
     const float *dt_bias;
     const float *conv_w;     // [C][K]
     float *raw_out;          // [rows][Hv*Dv]
+    // chunked prefill: one record of kRecFloats per (chunk, value head), chunk
+    // records of a sequence from meta.chunk0 on
+    float *chunk_rec;
     // KEEP_ROWS calls (gdn_head_kernel only): per (slot, row) the row's decay
     // alpha [Hv], correction delta [Hv][Dv], normalised key k^ [Hv][Dk] and raw
     // conv inputs x [C], from which gdn_rollback_kernel rebuilds the state and
@@ -84,6 +88,12 @@ struct ConvChan {
         for (int j = 0; j < kMaxK - 1; ++j) hist[j] = history_row[j < last_h ? j : last_h];
 #pragma unroll
         for (int j = 0; j < kMaxK; ++j) w[j] = weights[j < (int)K - 1 ? j : (int)K - 1];
+    }
+    // the K-1 raw inputs before the next row from src[j * stride], oldest first
+    __device__ __forceinline__ void set_hist(const float *src, int stride, uint32_t K) {
+        const int last_h = K >= 2 ? (int)K - 2 : 0;
+#pragma unroll
+        for (int j = 0; j < kMaxK - 1; ++j) hist[j] = src[(j < last_h ? j : last_h) * stride];
     }
     static constexpr int kK = 0;  // kernel size known only at run time
     // silu(sum_{j<K-1} hist[j] * w[j] + x * w[K-1]), then append x
@@ -577,7 +587,7 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 }
 
 // ---------------------------------------------------------------------------
-// gdn_chunk_kernel: the delta rule of prefill-sized calls in chunked form on
+// Chunked prefill: the delta rule of prefill-sized calls in chunked form on
 // f32 MFMA (v_mfma_f32_16x16x4f32).  With k^, q^ the L2-normalised conv
 // outputs, g_t = sum_{i<=t} log(alpha_i) over the chunk and S0 the state at
 // the chunk start, the token-serial recurrence (math.rs:222-236)
@@ -591,10 +601,20 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 //     Delta = U - W S0^T
 //     o_t   = (e^{g_t} S0 q^_t + sum_{j<=t} e^{g_t-g_j} (q^_t . k^_j) delta_j) / sqrt(Dk)
 //     S_C   = e^{g_C} S0 + sum_j e^{g_C-g_j} delta_j k^_j^T.
-// Decays enter only as e^{x} with x <= 0.  One workgroup per (sequence,
-// value head, 32 of the Dv = 128 state rows): rows of S are independent, so
-// the state slice stays in LDS for all chunks of the call; the chunk-wide
-// products (q.k, k.k, T, W) are recomputed by the four workgroups of a head.
+// Decays enter only as e^{x} with x <= 0.
+//
+// Only the three products with S0 depend on the state.  Everything else --
+// conv, norms, q.k, k.k, T, W, U -- depends on the chunk's own rows and the
+// K-1 raw inputs before them, so it is computed in two kernels:
+//   gdn_chunk_prep_kernel: one workgroup per (sequence, chunk, value head),
+//     all chunks of the call at once; writes a record per (chunk, value head):
+//       Qe = diag(e^{g_t} / |q_t|) Q,  -W,  U,  Ks = K^T diag(e^{g_C-g_j} / |k_j|),
+//       Pm[t][j] = e^{g_t-g_j} (q^_t . k^_j) (j <= t),  e^{g_C}
+//     and, from the last chunk, the next conv history;
+//   gdn_chunk_scan_kernel: one workgroup per (sequence, value head, 32 of the
+//     Dv = 128 state rows), the slice in LDS, walking the chunks in order:
+//       Delta = U + (-W) S0^T,  o = (Qe S0^T + Pm Delta) / sqrt(Dk),
+//       S_C = e^{g_C} S0 + Delta^T Ks^T.
 // The conv history is double-buffered exactly as in gdn_delta_kernel.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -609,8 +629,8 @@ constexpr int kCk = 32;        // rows per chunk
 constexpr int kVs = 32;        // state rows (value dims) per workgroup
 constexpr int kPr = kDk + 4;   // pitch (floats) of [.][Dk] arrays
 constexpr int kPc = kCk + 4;   // pitch of [.][chunk] arrays
-constexpr int kChunkThreads = 256;
-constexpr int kXin = 2 * kDk + kVs;  // conv channels a workgroup reads
+constexpr int kScanThreads = 512;  // gdn_chunk_scan_kernel
+constexpr int kPrepThreads = 512;  // gdn_chunk_prep_kernel
 
 // x * sigmoid(x) with the hardware exp2 and reciprocal (a few ulp from the
 // libm form; the chunked path is held to the f32 tolerance, not to ulps)
@@ -618,24 +638,46 @@ __device__ __forceinline__ float fast_silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
-struct ChunkLds {
-    float s0[kVs][kPr];   // state slice: rows v, dims d
-    float q[kCk][kPr];    // conv(q) rows t; later -W
-    float k[kCk][kPr];    // conv(k) rows t
-    float kc[kDk][kPc];   // conv(k) transposed: [d][t]
-    float vc[kVs][kPc];   // conv(v) of the slice transposed: [v][t]
-    float a[kCk][kPc];    // A (strictly lower)
-    float t[kCk][kPc];    // T = (I + A)^-1
-    float pm[kCk][kPc];   // e^{g_t-g_j} (q^_t . k^_j), j <= t
-    float dt[kVs][kPc];   // Delta transposed: [v][t]
-    float g[kCk];         // cumulative log decay
+// One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.
+constexpr int kRecQe = 0;                      // [kCk][kDk]     Qe
+constexpr int kRecWn = kRecQe + kCk * kDk;     // [kCk][kDk]     -W
+constexpr int kRecU = kRecWn + kCk * kDk;      // [kCk][kHeadDv] U
+constexpr int kRecKs = kRecU + kCk * kHeadDv;  // [kDk][kCk]     Ks
+constexpr int kRecPm = kRecKs + kDk * kCk;     // [kCk][kCk]     Pm
+constexpr int kRecEc = kRecPm + kCk * kCk;     // e^{g_C}
+constexpr int kRecFloats = kRecEc + 64;        // a 256-byte multiple
+constexpr int kPre = kMaxK - 1;                // raw input rows staged before a chunk
+constexpr int kPin = 2 * kDk + kHeadDv;        // raw input channels of a (chunk, value head)
+
+struct PrepLds {
+    float q[kCk][kPr];        // conv(q) rows t
+    float k[kCk][kPr];        // conv(k) rows t
+    float kc[kDk][kPc];       // conv(k) transposed: [d][t]
+    float vc[kHeadDv][kPc];   // conv(v) transposed: [v][t]
+    float a[kCk][kPc];        // A (strictly lower)
+    float t[kCk][kPc];        // T = (I + A)^-1
+    float tt[kCk][kPc];       // T11^T, then M^T (P2 scratch)
+    float g[kCk];             // cumulative log decay
     float beta[kCk];
-    float rq[kCk];        // 1 / |q_t|
-    float rk[kCk];        // 1 / |k_t|
-    float sw[kCk];        // column scales of T: beta_j e^{g_j} / |k_j| (W)
-    float su[kCk];        //   beta_j (U)
-    float ss[kCk];        //   e^{g_C - g_j} / |k_j| (state update; g_C: last row)
-    float xin[kCk][kXin]; // raw conv inputs of the chunk: q, k, then the v slice
+    float rq[kCk];            // 1 / |q_t|
+    float rk[kCk];            // 1 / |k_t|
+    float sw[kCk];            // column scales of T: beta_j e^{g_j} / |k_j| (W)
+    float su[kCk];            //   beta_j (U)
+    float ss[kCk];            //   e^{g_C - g_j} / |k_j| (Ks; g_C: last row)
+    float qs[kCk];            // Qe's row scales e^{g_t} / |q_t|
+    float xin[kPre + kCk][kPin];  // raw inputs: kPre rows before the chunk, then its rows
+};
+
+struct ScanLds {
+    float s0[kVs][kPr];  // state slice: rows v, dims d
+    float dt[kVs][kPc];  // Delta of the slice, transposed: [v][t]
+    struct Rec {         // a chunk's record, rows padded against bank conflicts
+        float qe[kCk][kPr];
+        float wn[kCk][kPr];
+        float ks[kDk][kPc];
+        float pm[kCk][kPc];
+        float u[kCk][kPc];  // this slice's columns of U
+    } r[2];
 };
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
@@ -696,6 +738,10 @@ struct ConvK {
 #pragma unroll
         for (int j = 0; j < K; ++j) w[j] = weights[j];
     }
+    __device__ __forceinline__ void set_hist(const float *src, int stride, uint32_t) {
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) hist[j] = src[j * stride];
+    }
     __device__ __forceinline__ float pre(float x, uint32_t) {
         float acc = 0.0f;
 #pragma unroll
@@ -727,205 +773,63 @@ __device__ __forceinline__ float pick(const float (&a)[N], int i) {
 }
 
 template <class Conv>
-__global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParams p) {
+__global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnParams p) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    ChunkLds &L = *(ChunkLds *)lds_raw;
+    PrepLds &L = *(PrepLds *)lds_raw;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int r16 = lane & 15;
     const int sl = lane >> 4;
-    const int tr = wave >> 1, tc = wave & 1;  // this wave's tile of the products
 
-    const uint32_t nq = p.value_dim / kVs;  // state-row blocks per head
-    const uint32_t vq = blockIdx.x % nq;
-    const uint32_t h = (blockIdx.x / nq) % p.value_heads;
-    const GdnMeta m = p.meta[blockIdx.x / (nq * p.value_heads)];
+    const uint32_t h = blockIdx.x;
+    const uint32_t c = blockIdx.y;
+    const GdnMeta m = p.meta[blockIdx.z];
+    const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
+    if (c >= nchunks) return;
+    const uint32_t r0 = c * kCk;
+    const uint32_t nv = min((uint32_t)kCk, m.rows - r0);
+    float *rec = p.chunk_rec + ((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats;
     const uint32_t groups = p.value_heads / p.key_heads;
     const uint32_t kh = h / groups;
     const uint32_t key_width = p.key_heads * kDk;
     const uint32_t K1 = p.conv_k - 1;
     const bool bf16_in = p.bf16_in != 0;
-
-    // conv channels: thread tid < 128 q dim tid, tid < 256 k dim tid - 128,
-    // over all rows of a chunk; lanes 0..31 of every wave also the 32 v
-    // channels of the slice over their wave's 8 rows of the chunk
-    constexpr int KC = Conv::kK;                   // 0: run-time kernel size
-    constexpr int KW = KC ? KC : kMaxK;            // window bound
+    constexpr int KC = Conv::kK;  // 0: run-time kernel size
     const int Kr = KC ? KC : (int)p.conv_k;
-    const uint32_t ch0 = tid < kDk ? kh * kDk + tid : key_width + kh * kDk + (tid - kDk);
-    const int cvl = lane & 31;
-    const uint32_t ch1 = 2 * key_width + h * p.value_dim + vq * kVs + cvl;
+
+    // conv work of this thread (the row ranges are wave-uniform): q/k channel
+    // qc (q dim qc < 128, else k dim qc - 128) over rows 16 qhalf .. + 15, and
+    // v channel vch over rows 8 vquart .. + 7
+    const int qc = tid & (2 * kDk - 1);
+    const int qhalf = tid >> 8;
+    const int vch = tid & (kHeadDv - 1);
+    const int vquart = tid >> 7;
+    const uint32_t ch0 = qc < kDk ? kh * kDk + qc : key_width + kh * kDk + (qc - kDk);
+    const uint32_t ch1 = 2 * key_width + h * kHeadDv + vch;
     const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
     const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
-    Conv cv0;
+    // weights and the stored history (used by the rows that start the call;
+    // the others take the K-1 inputs before them from the staged rows)
+    Conv cv0, cvv;
     cv0.load(p.history + (hist_slot + ch0) * K1, p.conv_w + (size_t)ch0 * p.conv_k, p.conv_k);
-    // the v channel: weights and the K-1 inputs before the chunk
-    float wv[KW], hv[KW > 1 ? KW - 1 : 1];
-#pragma unroll
-    for (int j = 0; j < KW; ++j) wv[j] = p.conv_w[(size_t)ch1 * p.conv_k + min(j, Kr - 1)];
-#pragma unroll
-    for (int j = 0; j < KW - 1; ++j) hv[j] = p.history[(hist_slot + ch1) * K1 + min(j, max(Kr - 2, 0))];
+    cvv.load(p.history + (hist_slot + ch1) * K1, p.conv_w + (size_t)ch1 * p.conv_k, p.conv_k);
 
-    // state slice -> LDS (16 floats per thread, as 4 spans of 4 that are 32
-    // floats apart: each 16-byte access instruction covers 128 contiguous
-    // bytes of a row)
-    float *state = p.state + (((size_t)m.state_in * p.value_heads + h) * p.value_dim + vq * kVs) * kDk;
+    // decay and write strength inputs first: wave 1 turns them into g and
+    // beta while the raw inputs below are in flight
+    const int cvl = lane & 31;
+    float av = 0.0f, bv = 0.0f;
     {
-        const int v = tid >> 3, d0 = (tid & 7) * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(float4 *)&L.s0[v][d0 + 32 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 32 * i);
-        }
+        const size_t row = (size_t)m.row0 + r0 + min((uint32_t)cvl, nv - 1);
+        av = load_act_nb(p.a, row * p.value_heads + h, bf16_in);
+        bv = load_act_nb(p.b, row * p.value_heads + h, bf16_in);
     }
     const float a_log_e = expf(p.a_log[h]);
     const float dt_bias = p.dt_bias[h];
-    const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
-
-    for (uint32_t r0 = 0; r0 < m.rows; r0 += kCk) {
-        const uint32_t nv = min((uint32_t)kCk, m.rows - r0);
-        const size_t row0 = (size_t)m.row0 + r0;
-        // ---- raw inputs of the chunk -> LDS in 16-byte segments of the
-        //      three channel ranges (q, k of the key head; the v slice), every
-        //      load in flight together; rows past nv repeat the last valid
-        //      row and are not used.  The lane id is re-pinned per chunk so
-        //      that the segment offsets are recomputed, not held live.
-        {
-            uint32_t lt = tid;
-            pin(lt);
-            auto seg_src = [&](int t, int c0) -> size_t {
-                const uint32_t ch = c0 < kDk ? kh * kDk + c0
-                                  : c0 < 2 * kDk ? key_width + kh * kDk + (c0 - kDk)
-                                                 : 2 * key_width + h * p.value_dim + vq * kVs + (c0 - 2 * kDk);
-                return (row0 + min((uint32_t)t, nv - 1)) * p.channels + ch;
-            };
-            if (!bf16_in) {
-                constexpr int SEG = kXin / 4;                       // per row
-                constexpr int N = kCk * SEG / kChunkThreads;        // per thread
-                static_assert(kCk * SEG % kChunkThreads == 0, "segments");
-                f32x4 xs[N];
-#pragma unroll
-                for (int n = 0; n < N; ++n) {
-                    const int e = lt + n * kChunkThreads;
-                    xs[n] = *(const f32x4 *)((const float *)p.qkv + seg_src(e / SEG, 4 * (e % SEG)));
-                }
-#pragma unroll
-                for (int n = 0; n < N; ++n) {
-                    const int e = lt + n * kChunkThreads;
-                    *(f32x4 *)&L.xin[e / SEG][4 * (e % SEG)] = xs[n];
-                }
-            } else {
-                constexpr int SEG = kXin / 8;
-                constexpr int N = (kCk * SEG + kChunkThreads - 1) / kChunkThreads;
-                u32x4 xs[N];
-#pragma unroll
-                for (int n = 0; n < N; ++n) {
-                    const int e = min((int)lt + n * kChunkThreads, kCk * SEG - 1);
-                    xs[n] = *(const u32x4 *)((const uint16_t *)p.qkv + seg_src(e / SEG, 8 * (e % SEG)));
-                }
-#pragma unroll
-                for (int n = 0; n < N; ++n) {
-                    const int e = (int)lt + n * kChunkThreads;
-                    if (e < kCk * SEG) {
-                        float *dst = &L.xin[e / SEG][8 * (e % SEG)];
-                        *(f32x4 *)dst = f32x4{__uint_as_float(xs[n][0] << 16), __uint_as_float(xs[n][0] & 0xffff0000u),
-                                              __uint_as_float(xs[n][1] << 16), __uint_as_float(xs[n][1] & 0xffff0000u)};
-                        *(f32x4 *)(dst + 4) = f32x4{__uint_as_float(xs[n][2] << 16), __uint_as_float(xs[n][2] & 0xffff0000u),
-                                                    __uint_as_float(xs[n][3] << 16), __uint_as_float(xs[n][3] & 0xffff0000u)};
-                    }
-                }
-            }
-        }
-        float av = 0.0f, bv = 0.0f;
-        {
-            const size_t row = row0 + min((uint32_t)cvl, nv - 1);
-            av = load_act_nb(p.a, row * p.value_heads + h, bf16_in);
-            bv = load_act_nb(p.b, row * p.value_heads + h, bf16_in);
-        }
-        __syncthreads();
-        // ---- causal conv + silu (math.rs:158-187); rows past nv are zero
-        //      and do not advance the history.  Each phase reads its LDS
-        //      inputs into registers first, then computes, then stores.
-        const bool full = nv == (uint32_t)kCk;
-        {
-            float xr[kCk];
-#pragma unroll
-            for (int t = 0; t < kCk; ++t) xr[t] = L.xin[t][tid];
-            float yr[kCk];
-            if (full) {
-#pragma unroll
-                for (int t = 0; t < kCk; ++t) yr[t] = fast_silu(cv0.pre(xr[t], p.conv_k));
-            } else {
-#pragma unroll
-                for (int t = 0; t < kCk; ++t) {
-                    yr[t] = 0.0f;
-                    if ((uint32_t)t < nv) yr[t] = fast_silu(cv0.pre(xr[t], p.conv_k));
-                }
-            }
-            if (tid < kDk) {
-#pragma unroll
-                for (int t = 0; t < kCk; ++t) L.q[t][tid] = yr[t];
-            } else {
-#pragma unroll
-                for (int t = 0; t < kCk; ++t) L.k[t][tid - kDk] = yr[t];
-#pragma unroll
-                for (int t = 0; t < kCk; t += 4) {
-                    *(f32x4 *)&L.kc[tid - kDk][t] = f32x4{yr[t], yr[t + 1], yr[t + 2], yr[t + 3]};
-                }
-            }
-        }
-        {
-            // v channel cvl, rows tb .. tb + 7 (tb = 8 wave): the window of
-            // row t is position t + j (tap j) of (hv, x_0, x_1, ...); only
-            // wave 0's rows reach into hv
-            const int tb = 8 * wave;
-            constexpr int NW = 8 + KW - 1;
-            float xw[NW];  // positions tb .. tb + NW - 1 of (hv, x)
-#pragma unroll
-            for (int i = 0; i < NW; ++i) {
-                const int u = tb + i - (Kr - 1);  // input row
-                xw[i] = L.xin[min(max(u, 0), kCk - 1)][2 * kDk + cvl];
-                if (wave == 0 && i < KW - 1) {
-                    if (i < Kr - 1) xw[i] = hv[i < KW - 1 ? i : 0];
-                }
-            }
-            float yv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KW; ++j) {
-                    if (j < Kr) acc += xw[i + j] * wv[j];
-                }
-                yv[i] = (uint32_t)(tb + i) < nv ? fast_silu(acc) : 0.0f;
-            }
-            if (lane < kVs) {
-                *(f32x4 *)&L.vc[lane][tb] = f32x4{yv[0], yv[1], yv[2], yv[3]};
-                *(f32x4 *)&L.vc[lane][tb + 4] = f32x4{yv[4], yv[5], yv[6], yv[7]};
-            }
-            // the history after the chunk: the last K-1 of (hv, x_0 .. x_{nv-1})
-            if (full) {
-#pragma unroll
-                for (int j = 0; j < KW - 1; ++j) {
-                    if (j < Kr - 1) hv[j] = L.xin[kCk - (Kr - 1) + j][2 * kDk + cvl];
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < kCk; ++t) {
-                    if ((uint32_t)t < nv) {
-                        const float x = L.xin[t][2 * kDk + cvl];
-#pragma unroll
-                        for (int j = 0; j < KW - 1; ++j) {
-                            if (j + 2 < Kr) hv[j] = hv[j + 1];
-                            else if (j + 2 == Kr) hv[j] = x;
-                        }
-                    }
-                }
-            }
-        }
+    auto decay_and_strength = [&]() __attribute__((always_inline)) {
         if (wave == 1) {
-            // decay and write strength (math.rs:220-221); padded rows: alpha 1, beta 0
+            // math.rs:220-221; padded rows: alpha 1, beta 0
             const bool valid = (uint32_t)cvl < nv;
             float la = valid ? -a_log_e * softplus_ref(av + dt_bias) : 0.0f;
             const float beta = valid ? ref_sigmoid(bv) : 0.0f;
@@ -939,254 +843,499 @@ __global__ void __launch_bounds__(kChunkThreads) gdn_chunk_kernel(const GdnParam
                 L.beta[lane] = beta;
             }
         }
-        __syncthreads();
-        // ---- L2 norms of q and k per row (math.rs:218-219): 8 lanes per
-        //      row, 16 dims each, then a reduction over the 8
-        {
-            const int t = 8 * wave + (lane >> 3), part = lane & 7;
-            float sq = 0.0f, sk = 0.0f;
+    };
+    // ---- raw inputs: rows r0 - kPre .. r0 + kCk - 1 of the sequence, clamped
+    //      into its rows (clamped copies are never used), in 16-byte segments
+    //      of the three channel ranges, every load in flight together
+    {
+        uint32_t lt = tid;
+        pin(lt);
+        auto seg_src = [&](int rr, int c0) -> size_t {
+            const uint32_t ch = c0 < kDk ? kh * kDk + c0
+                              : c0 < 2 * kDk ? key_width + kh * kDk + (c0 - kDk)
+                                             : 2 * key_width + h * kHeadDv + (c0 - 2 * kDk);
+            const int row = min(max((int)r0 - kPre + rr, 0), (int)m.rows - 1);
+            return ((size_t)m.row0 + row) * p.channels + ch;
+        };
+        constexpr int R = kPre + kCk;
+        if (!bf16_in) {
+            constexpr int SEG = kPin / 4;
+            constexpr int N = (R * SEG + kPrepThreads - 1) / kPrepThreads;
+            f32x4 xs[N];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 a4 = *(const float4 *)&L.q[t][16 * part + 4 * i];
-                const float4 b4 = *(const float4 *)&L.k[t][16 * part + 4 * i];
-                sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
-                sk += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
+            for (int n = 0; n < N; ++n) {
+                const int e = min((int)lt + n * kPrepThreads, R * SEG - 1);
+                xs[n] = *(const f32x4 *)((const float *)p.qkv + seg_src(e / SEG, 4 * (e % SEG)));
             }
+            decay_and_strength();
 #pragma unroll
-            for (int o = 1; o < 8; o <<= 1) {
-                sq += __shfl_xor(sq, o);
-                sk += __shfl_xor(sk, o);
+            for (int n = 0; n < N; ++n) {
+                const int e = (int)lt + n * kPrepThreads;
+                if (e < R * SEG) *(f32x4 *)&L.xin[e / SEG][4 * (e % SEG)] = xs[n];
             }
-            if (part == 0) {
-                L.rq[t] = 1.0f / sqrtf(sq + 1e-6f);
-                L.rk[t] = 1.0f / sqrtf(sk + 1e-6f);
-            }
-        }
-        __syncthreads();
-        // ---- P1: q.k, k.k and q.S0 tiles; wave w owns tile (w >> 1, w & 1)
-        //      (the three accumulation chains interleaved)
-        f32x4 oq = {0, 0, 0, 0};
-        {
-            f32x4 sqk = {0, 0, 0, 0}, akk = {0, 0, 0, 0};
+        } else {
+            constexpr int SEG = kPin / 8;
+            constexpr int N = (R * SEG + kPrepThreads - 1) / kPrepThreads;
+            u32x4 xs[N];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-            constexpr int NH = kDk / 32;
-            Ops<NH> qa, kb, sb, ka;
-            load_ops(qa, &L.q[16 * tr][NH * 16 * half], kPr, lane);
-            load_ops(kb, &L.k[16 * tc][NH * 16 * half], kPr, lane);
-            load_ops(sb, &L.s0[16 * tc][NH * 16 * half], kPr, lane);
-            load_ops(ka, &L.k[16 * tr][NH * 16 * half], kPr, lane);
-#pragma unroll
-            for (int st = 0; st < NH; ++st) {
-                sqk = mfma4(qa.v[st].x, kb.v[st].x, sqk);
-                oq = mfma4(qa.v[st].x, sb.v[st].x, oq);
-                akk = mfma4(ka.v[st].x, kb.v[st].x, akk);
-                sqk = mfma4(qa.v[st].y, kb.v[st].y, sqk);
-                oq = mfma4(qa.v[st].y, sb.v[st].y, oq);
-                akk = mfma4(ka.v[st].y, kb.v[st].y, akk);
-                sqk = mfma4(qa.v[st].z, kb.v[st].z, sqk);
-                oq = mfma4(qa.v[st].z, sb.v[st].z, oq);
-                akk = mfma4(ka.v[st].z, kb.v[st].z, akk);
-                sqk = mfma4(qa.v[st].w, kb.v[st].w, sqk);
-                oq = mfma4(qa.v[st].w, sb.v[st].w, oq);
-                akk = mfma4(ka.v[st].w, kb.v[st].w, akk);
+            for (int n = 0; n < N; ++n) {
+                const int e = min((int)lt + n * kPrepThreads, R * SEG - 1);
+                xs[n] = *(const u32x4 *)((const uint16_t *)p.qkv + seg_src(e / SEG, 8 * (e % SEG)));
             }
-            }
-            const int j = 16 * tc + r16;
-            const float gj = L.g[j], rkj = L.rk[j];
+            decay_and_strength();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * tr + 4 * sl + i;
-                const float gt = L.g[t];
-                const float e = expf(j <= t ? gt - gj : -INFINITY);
-                L.pm[t][j] = e * L.rq[t] * rkj * sqk[i];
-                L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * akk[i] : 0.0f;
-                oq[i] *= L.rq[t] * expf(gt);  // e^{g_t} S0 q^_t
+            for (int n = 0; n < N; ++n) {
+                const int e = (int)lt + n * kPrepThreads;
+                if (e < R * SEG) {
+                    float *dst = &L.xin[e / SEG][8 * (e % SEG)];
+                    *(f32x4 *)dst = f32x4{__uint_as_float(xs[n][0] << 16), __uint_as_float(xs[n][0] & 0xffff0000u),
+                                          __uint_as_float(xs[n][1] << 16), __uint_as_float(xs[n][1] & 0xffff0000u)};
+                    *(f32x4 *)(dst + 4) = f32x4{__uint_as_float(xs[n][2] << 16), __uint_as_float(xs[n][2] & 0xffff0000u),
+                                                __uint_as_float(xs[n][3] << 16), __uint_as_float(xs[n][3] & 0xffff0000u)};
+                }
             }
         }
-        __syncthreads();
-        // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
-        //      blocks by forward substitution (lane j: column j), storing T
-        //      and its transpose; wave 2 clears the upper-right block and
-        //      wave 3 computes the column scales.
-        if (wave < 2) {
-            const int b0 = 16 * wave;
-            const int j = r16;
-            // the block's strict lower triangle, in registers first
-            f32x4 ar[16][4];
+    }
+    __syncthreads();
+    // ---- causal conv + silu (math.rs:158-187); rows past nv are zero and do
+    //      not advance the history
+    if (c > 0 || qhalf == 1) cv0.set_hist(&L.xin[kPre + 16 * qhalf - (Kr - 1)][qc], kPin, p.conv_k);
+    if (c > 0 || vquart > 0) {
+        cvv.set_hist(&L.xin[kPre + 8 * vquart - (Kr - 1)][2 * kDk + vch], kPin, p.conv_k);
+    }
+    {
+        const int tb = 16 * qhalf;
+        float xr[16];
 #pragma unroll
-            for (int i = 1; i < 16; ++i)
+        for (int i = 0; i < 16; ++i) xr[i] = L.xin[kPre + tb + i][qc];
+        float yr[16];
+        if (tb + 16 <= (int)nv) {
 #pragma unroll
-                for (int qd = 0; 4 * qd < i; ++qd) ar[i][qd] = *(const f32x4 *)&L.a[b0 + i][b0 + 4 * qd];
-            float x[16];
+            for (int i = 0; i < 16; ++i) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
+        } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float acc0 = i == j ? 1.0f : 0.0f, acc1 = 0.0f;
-#pragma unroll
-                for (int mm = 0; mm < i; ++mm) {
-                    const float am = ar[i][mm >> 2][mm & 3];
-                    if (mm & 1) acc1 -= am * x[mm];
-                    else acc0 -= am * x[mm];
-                }
-                x[i] = acc0 + acc1;
+                yr[i] = 0.0f;
+                if ((uint32_t)(tb + i) < nv) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
             }
-            if (lane < 16) {
+        }
+        if (qc < kDk) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    L.t[b0 + i][b0 + j] = x[i];
-                    L.dt[b0 + j][b0 + i] = x[i];  // T^T (dt is free until P4)
-                }
+            for (int i = 0; i < 16; ++i) L.q[tb + i][qc] = yr[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) L.k[tb + i][qc - kDk] = yr[i];
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                *(f32x4 *)&L.kc[qc - kDk][tb + i] = f32x4{yr[i], yr[i + 1], yr[i + 2], yr[i + 3]};
             }
-        } else if (wave == 2) {
-            for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
-        } else if (lane < kCk) {
-            // W uses beta_j e^{g_j} / |k_j|, U beta_j, the state update
-            // e^{g_C - g_j} / |k_j| (g_C: the last row's g)
-            const float gj = L.g[lane], rkj = L.rk[lane];
-            L.sw[lane] = L.beta[lane] * expf(gj) * rkj;
-            L.su[lane] = L.beta[lane];
-            L.ss[lane] = expf(L.g[kCk - 1] - gj) * rkj;
         }
-        __syncthreads();
-        //      T21 = -T22 A21 T11 (wave 0): M = A21 T11 with B = T11^T rows,
-        //      M^T through LDS (pm rows are read only in P5; use a scratch
-        //      block of dt), then T21 = -T22 M.
-        if (wave == 0) {
-            Ops<1> a21, t11t;
-            load_ops(a21, &L.a[16][0], kPc, lane);
-            load_ops(t11t, &L.dt[0][0], kPc, lane);
-            f32x4 mt = {0, 0, 0, 0};
-            mma(mt, a21, t11t);
+    }
+    {
+        const int tb = 8 * vquart;
+        float xr[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) L.dt[16 + r16][4 * sl + i] = mt[i];  // M^T
-            Ops<1> t22, mtr;
-            load_ops(t22, &L.t[16][16], kPc, lane);
-            load_ops(mtr, &L.dt[16][0], kPc, lane);
-            f32x4 t21 = {0, 0, 0, 0};
-            mma(t21, t22, mtr);
+        for (int i = 0; i < 8; ++i) xr[i] = L.xin[kPre + tb + i][2 * kDk + vch];
+        float yv[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
+        for (int i = 0; i < 8; ++i) {
+            yv[i] = 0.0f;
+            if ((uint32_t)(tb + i) < nv) yv[i] = fast_silu(cvv.pre(xr[i], p.conv_k));
         }
-        __syncthreads();
-        // ---- P3: W = T diag(sw) K (stored negated over q, which nobody
-        //      reads after P1) and U = T diag(su) V (this wave's Delta
-        //      accumulator)
-        f32x4 du = {0, 0, 0, 0};
-        {
-            Ops<2> tw, tu, vb;
-            load_ops(tw, &L.t[16 * tr][0], kPc, lane);
-            tu = tw;
-            load_ops(vb, &L.vc[16 * tc][0], kPc, lane);
-            Ops<2> kb4[4];
+        *(f32x4 *)&L.vc[vch][tb] = f32x4{yv[0], yv[1], yv[2], yv[3]};
+        *(f32x4 *)&L.vc[vch][tb + 4] = f32x4{yv[4], yv[5], yv[6], yv[7]};
+    }
+    // the history after the call: the last K-1 raw inputs, from the last
+    // chunk, by the threads whose rows hold the last row (q/k channels only
+    // in the first value head of the key head)
+    if (c + 1 == nchunks) {
+        if (h % groups == 0 && qhalf == (nv > 16 ? 1 : 0)) cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
+        if (vquart == (int)(nv - 1) / 8) cvv.store(p.history + (hist_next + ch1) * K1, p.conv_k);
+    }
+    __syncthreads();
+    // ---- L2 norms of q and k per row (math.rs:218-219): 16 lanes per row,
+    //      8 dims each, then a reduction over the 16; and Qe's row scale
+    //      e^{g_t} / |q_t|
+    {
+        const int t = 4 * wave + (lane >> 4), part = lane & 15;
+        float sq = 0.0f, sk = 0.0f;
 #pragma unroll
-            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &L.kc[64 * tc + 16 * n][0], kPc, lane);
-            scale_ops(tw, L.sw, lane);
-            scale_ops(tu, L.su, lane);
-            f32x4 w[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+        for (int i = 0; i < 2; ++i) {
+            const float4 a4 = *(const float4 *)&L.q[t][8 * part + 4 * i];
+            const float4 b4 = *(const float4 *)&L.k[t][8 * part + 4 * i];
+            sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
+            sk += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
+        }
+        sq = sum16(sq);
+        sk = sum16(sk);
+        if (part == 0) {
+            const float rq = 1.0f / sqrtf(sq + 1e-6f);
+            L.rq[t] = rq;
+            L.rk[t] = 1.0f / sqrtf(sk + 1e-6f);
+            L.qs[t] = rq * expf(L.g[t]);
+        }
+    }
+    __syncthreads();
+    // ---- P1: the q.k and k.k tiles on or below the diagonal, one per wave:
+    //      waves 0..2 k.k tiles (0,0), (1,0), (1,1) -> A; waves 3..5 the same
+    //      q.k tiles -> Pm (wave 3 also writes Pm's zero tile (0, 1)); waves
+    //      6 and 7 write Qe = diag(e^{g_t} / |q_t|) Q.
+    if (wave < 6) {
+        const int tile = wave % 3;
+        const int tr = tile == 0 ? 0 : 1, tc = tile == 2 ? 1 : 0;
+        const bool is_kk = wave < 3;
+        const float *arow = is_kk ? &L.k[16 * tr][0] : &L.q[16 * tr][0];
+        f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
 #pragma unroll
-            for (int st = 0; st < 2; ++st)
+        for (int half = 0; half < 2; ++half) {
+            constexpr int NH = kDk / 32;
+            Ops<NH> xa, kb;
+            load_ops(xa, arow + NH * 16 * half, kPr, lane);
+            load_ops(kb, &L.k[16 * tc][NH * 16 * half], kPr, lane);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    du = mfma4(tu.v[st][e], vb.v[st][e], du);
+            for (int st = 0; st < NH; ++st) {
+                acc = mfma4(xa.v[st].x, kb.v[st].x, acc);
+                acc2 = mfma4(xa.v[st].y, kb.v[st].y, acc2);
+                acc = mfma4(xa.v[st].z, kb.v[st].z, acc);
+                acc2 = mfma4(xa.v[st].w, kb.v[st].w, acc2);
+            }
+        }
+        const int j = 16 * tc + r16;
+        const float gj = L.g[j], rkj = L.rk[j];
 #pragma unroll
-                    for (int n = 0; n < 4; ++n) w[n] = mfma4(tw.v[st][e], kb4[n].v[st][e], w[n]);
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * tr + 4 * sl + i;
+            const float gt = L.g[t];
+            const float e = expf(j <= t ? gt - gj : -INFINITY);
+            const float x = acc[i] + acc2[i];
+            if (is_kk) {
+                L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * x : 0.0f;
+            } else {
+                rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * x;
+            }
+        }
+        if (wave == 3) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rec[kRecPm + (4 * sl + i) * kCk + 16 + r16] = 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const int e = tid - 6 * 64 + n * 128;
+            const int t = e >> 5, d = 4 * (e & 31);
+            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.q[t][d] * L.qs[t];
+        }
+    }
+    __syncthreads();
+    // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
+    //      blocks by forward substitution (lane j: column j), storing T and
+    //      its transpose; wave 2 clears the upper-right block and wave 3
+    //      computes the column scales and e^{g_C}.
+    if (wave < 2) {
+        const int b0 = 16 * wave;
+        const int j = r16;
+        f32x4 ar[16][4];
+#pragma unroll
+        for (int i = 1; i < 16; ++i)
+#pragma unroll
+            for (int qd = 0; 4 * qd < i; ++qd) ar[i][qd] = *(const f32x4 *)&L.a[b0 + i][b0 + 4 * qd];
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float acc0 = i == j ? 1.0f : 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int mm = 0; mm < i; ++mm) {
+                const float am = ar[i][mm >> 2][mm & 3];
+                if (mm & 1) acc1 -= am * x[mm];
+                else acc0 -= am * x[mm];
+            }
+            x[i] = acc0 + acc1;
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                L.t[b0 + i][b0 + j] = x[i];
+                L.tt[b0 + j][b0 + i] = x[i];
+            }
+        }
+    } else if (wave == 2) {
+        for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
+    } else if (wave == 3 && lane < kCk) {
+        const float gj = L.g[lane], rkj = L.rk[lane];
+        L.sw[lane] = L.beta[lane] * expf(gj) * rkj;
+        L.su[lane] = L.beta[lane];
+        L.ss[lane] = expf(L.g[kCk - 1] - gj) * rkj;
+        if (lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
+    }
+    __syncthreads();
+    //      T21 = -T22 A21 T11 (wave 0): M = A21 T11 with B = T11^T rows, M^T
+    //      through LDS, then T21 = -T22 M.  Waves 1..7 meanwhile write Ks.
+    if (wave == 0) {
+        Ops<1> a21, t11t;
+        load_ops(a21, &L.a[16][0], kPc, lane);
+        load_ops(t11t, &L.tt[0][0], kPc, lane);
+        f32x4 mt = {0, 0, 0, 0};
+        mma(mt, a21, t11t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) L.tt[16 + r16][4 * sl + i] = mt[i];  // M^T
+        Ops<1> t22, mtr;
+        load_ops(t22, &L.t[16][16], kPc, lane);
+        load_ops(mtr, &L.tt[16][0], kPc, lane);
+        f32x4 t21 = {0, 0, 0, 0};
+        mma(t21, t22, mtr);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
+    } else {
+        // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
+        for (int e = tid - 64; e < kDk * kCk / 4; e += kPrepThreads - 64) {
+            const int d = e >> 3, j = 4 * (e & 7);
+            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
+                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
+        }
+    }
+    __syncthreads();
+    // ---- P3: W = T diag(sw) K (stored negated) and U = T diag(su) V; wave w
+    //      owns rows 16 (w & 1).. and columns 32 (w >> 1) .. + 31 of both
+    {
+        const int tr = wave & 1, c0 = 32 * (wave >> 1);
+        Ops<2> tw, tu;
+        load_ops(tw, &L.t[16 * tr][0], kPc, lane);
+        tu = tw;
+        Ops<2> kb2[2], vb2[2];
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            load_ops(kb2[n], &L.kc[c0 + 16 * n][0], kPc, lane);
+            load_ops(vb2[n], &L.vc[c0 + 16 * n][0], kPc, lane);
+        }
+        scale_ops(tw, L.sw, lane);
+        scale_ops(tu, L.su, lane);
+        f32x4 w[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        f32x4 u[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int n = 0; n < 2; ++n) {
+                    w[n] = mfma4(tw.v[st][e], kb2[n].v[st][e], w[n]);
+                    u[n] = mfma4(tu.v[st][e], vb2[n].v[st][e], u[n]);
                 }
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+        for (int n = 0; n < 2; ++n)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) L.q[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = -w[n][i];
+            for (int i = 0; i < 4; ++i) {
+                const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
+                rec[kRecWn + t * kDk + col] = -w[n][i];
+                rec[kRecU + t * kHeadDv + col] = u[n][i];
+            }
+    }
+}
+
+// The scan over a sequence's chunks for one 32-row slice of a value head's
+// state, 8 waves: waves 0..3 own the output tiles (rows 16 (w >> 1)..,
+// state rows 16 (w & 1)..), waves 4..7 the Delta tiles of the same places
+// and then the state-update tiles (state rows 16 ((w - 4) >> 1)..,
+// dims 64 ((w - 4) & 1)..), so each SIMD runs one wave of each kind and the
+// same MFMA count in both phases.  Each chunk's record (Qe, -W, Pm, Ks and
+// this slice's U columns) is staged once per workgroup into LDS,
+// double-buffered: the loads for chunk c + 1 are issued into registers at
+// the start of chunk c and written to the other buffer at its end, so they
+// have a whole chunk to land.  xcd_map: the grid is ordered so that the four
+// slices of a (sequence, value head) get workgroup ids 8 apart, which the
+// dispatcher places on one XCD, so they share its L2 for the record.
+__global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnParams p,
+                                                                      uint32_t xcd_map) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    ScanLds &L = *(ScanLds *)lds_raw;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r16 = lane & 15;
+    const int sl = lane >> 4;
+    const bool out_wave = wave < 4;  // wave-uniform role
+    const int tr = (wave & 3) >> 1, tc = wave & 1;
+
+    constexpr uint32_t nq = kHeadDv / kVs;  // slices per head
+    const uint32_t b = blockIdx.x;
+    uint32_t pair, vq;
+    if (xcd_map) {
+        vq = (b >> 3) % nq;
+        pair = ((b >> 3) / nq) * 8 + (b & 7);
+    } else {
+        vq = b % nq;
+        pair = b / nq;
+    }
+    const uint32_t h = pair % p.value_heads;
+    const GdnMeta m = p.meta[pair / p.value_heads];
+    const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
+    const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
+
+    // record staging: 7 16-byte segments per thread; segment e = tid + 512 n
+    // is in Qe (n < 2), -W (n < 4), Ks (n < 6), then Pm (waves 0..3) or U
+    constexpr int kSeg = 7;
+    auto rec_of = [&](uint32_t c) -> const float * {
+        return p.chunk_rec + ((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats;
+    };
+    const int t2 = tid & 255;
+    auto fetch = [&](const float *rec, f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < kSeg; ++n) {
+            const int e = tid + kScanThreads * (n & 1);
+            int src;
+            if (n < 2) src = kRecQe + (e >> 5) * kDk + 4 * (e & 31);
+            else if (n < 4) src = kRecWn + (e >> 5) * kDk + 4 * (e & 31);
+            else if (n < 6) src = kRecKs + (e >> 3) * kCk + 4 * (e & 7);
+            else if (out_wave) src = kRecPm + (t2 >> 3) * kCk + 4 * (t2 & 7);
+            else src = kRecU + (t2 >> 3) * kHeadDv + vq * kVs + 4 * (t2 & 7);
+            xs[n] = *(const f32x4 *)(rec + src);
+        }
+    };
+    auto put = [&](ScanLds::Rec &r, const f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < kSeg; ++n) {
+            const int e = tid + kScanThreads * (n & 1);
+            float *dst;
+            if (n < 2) dst = &r.qe[e >> 5][4 * (e & 31)];
+            else if (n < 4) dst = &r.wn[e >> 5][4 * (e & 31)];
+            else if (n < 6) dst = &r.ks[e >> 3][4 * (e & 7)];
+            else if (out_wave) dst = &r.pm[t2 >> 3][4 * (t2 & 7)];
+            else dst = &r.u[t2 >> 3][4 * (t2 & 7)];
+            *(f32x4 *)dst = xs[n];
+        }
+    };
+    f32x4 xs[kSeg];
+    fetch(rec_of(0), xs);
+    float *state = p.state + (((size_t)m.state_in * p.value_heads + h) * kHeadDv + vq * kVs) * kDk;
+    {
+        const int v = tid >> 4, d0 = (tid & 15) * 4;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            *(float4 *)&L.s0[v][d0 + 64 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 64 * i);
+        }
+    }
+    put(L.r[0], xs);
+    if (nchunks > 1) fetch(rec_of(1), xs);
+    __syncthreads();
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        const uint32_t r0 = c * kCk;
+        const uint32_t nv = min((uint32_t)kCk, m.rows - r0);
+        ScanLds::Rec &R = L.r[c & 1];
+        // phase 1, tile (rows 16 tr.., state rows 16 tc..): output waves
+        // Qe S0^T, Delta waves U + (-W) S0^T
+        Ops<kDk / 16> xa, sb;
+        load_ops(xa, out_wave ? &R.qe[16 * tr][0] : &R.wn[16 * tr][0], kPr, lane);
+        load_ops(sb, &L.s0[16 * tc][0], kPr, lane);
+        f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
+        if (!out_wave) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = R.u[16 * tr + 4 * sl + i][16 * tc + r16];
+        }
+#pragma unroll
+        for (int st = 0; st < kDk / 16; ++st)
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                acc = mfma4(xa.v[st][e], sb.v[st][e], acc);
+                acc2 = mfma4(xa.v[st][e + 1], sb.v[st][e + 1], acc2);
+            }
+        acc += acc2;
+        if (!out_wave) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.dt[16 * tc + r16][16 * tr + 4 * sl + i] = acc[i];
         }
         __syncthreads();
-        // ---- P4: Delta = U - W S0^T; stored transposed
-        {
-            Ops<kDk / 16> wa, sb;
-            load_ops(wa, &L.q[16 * tr][0], kPr, lane);
-            load_ops(sb, &L.s0[16 * tc][0], kPr, lane);
-            f32x4 d2 = {0, 0, 0, 0};
-#pragma unroll
-            for (int st = 0; st < kDk / 16; ++st)
-#pragma unroll
-                for (int e = 0; e < 4; e += 2) {
-                    du = mfma4(wa.v[st][e], sb.v[st][e], du);
-                    d2 = mfma4(wa.v[st][e + 1], sb.v[st][e + 1], d2);
-                }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) L.dt[16 * tc + r16][16 * tr + 4 * sl + i] = du[i] + d2[i];
-        }
-        __syncthreads();
-        // ---- P5: outputs, then the state at the chunk end
-        {
-            Ops<2> pa, db, da;
-            load_ops(pa, &L.pm[16 * tr][0], kPc, lane);
+        if (out_wave) {
+            // o += Pm Delta
+            Ops<2> pa, db;
+            load_ops(pa, &R.pm[16 * tr][0], kPc, lane);
             load_ops(db, &L.dt[16 * tc][0], kPc, lane);
+            mma(acc, pa, db);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t t = 16 * tr + 4 * sl + i;
+                if (t < nv) {
+                    p.raw_out[((size_t)m.row0 + r0 + t) * p.value_heads * kHeadDv + (size_t)h * kHeadDv +
+                              vq * kVs + 16 * tc + r16] = acc[i] * qscale;
+                }
+            }
+        } else {
+            // S_C = e^{g_C} S0 + Delta^T Ks^T over state rows 16 tr.., dims 64 tc..
+            const float eC = p.chunk_rec[((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats + kRecEc];
+            Ops<2> da;
             load_ops(da, &L.dt[16 * tr][0], kPc, lane);
             Ops<2> kb4[4];
 #pragma unroll
-            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &L.kc[64 * tc + 16 * n][0], kPc, lane);
+            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &R.ks[64 * tc + 16 * n][0], kPc, lane);
             float s0v[4][4];
 #pragma unroll
             for (int n = 0; n < 4; ++n)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s0v[n][i] = L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16];
-            scale_ops(da, L.ss, lane);
             f32x4 s4[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
             for (int st = 0; st < 2; ++st)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    oq = mfma4(pa.v[st][e], db.v[st][e], oq);
+                for (int e = 0; e < 4; ++e)
 #pragma unroll
                     for (int n = 0; n < 4; ++n) s4[n] = mfma4(da.v[st][e], kb4[n].v[st][e], s4[n]);
-                }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t t = 16 * tr + 4 * sl + i;
-                if (t < nv) {
-                    p.raw_out[(row0 + t) * p.value_heads * p.value_dim + (size_t)h * p.value_dim +
-                              vq * kVs + 16 * tc + r16] = oq[i] * qscale;
-                }
-            }
-            const float eC = expf(L.g[kCk - 1]);
-            __syncthreads();  // all reads of S0 are done
+            // each of these waves rewrites exactly the S0 elements it read
+            // into s0v; all other reads of S0 ended before the barrier above
 #pragma unroll
             for (int n = 0; n < 4; ++n)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = s4[n][i] + eC * s0v[n][i];
                 }
-            __syncthreads();  // the next chunk reads S0 and rewrites q, k, pm, ...
         }
+        // the next chunk's record into the other buffer (last read in the
+        // previous chunk), and the loads for the one after
+        if (c + 1 < nchunks) {
+            put(L.r[(c + 1) & 1], xs);
+            if (c + 2 < nchunks) fetch(rec_of(c + 2), xs);
+        }
+        __syncthreads();  // the next chunk reads S0, its record, and rewrites dt
     }
-    // state slice and history back (the same spans as the load)
     {
-        const int v = tid >> 3, d0 = (tid & 7) * 4;
+        const int v = tid >> 4, d0 = (tid & 15) * 4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            *(float4 *)(state + (size_t)v * kDk + d0 + 32 * i) = *(const float4 *)&L.s0[v][d0 + 32 * i];
-        }
-    }
-    const bool owns_qk = (h % groups == 0) && vq == 0;
-    if (owns_qk) cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
-    if (wave == 0 && lane < kVs) {
-#pragma unroll
-        for (int j = 0; j < KW - 1; ++j) {
-            if (j < Kr - 1) p.history[(hist_next + ch1) * K1 + j] = hv[j];
+        for (int i = 0; i < 2; ++i) {
+            *(float4 *)(state + (size_t)v * kDk + d0 + 64 * i) = *(const float4 *)&L.s0[v][d0 + 64 * i];
         }
     }
 }
 
 template <class Conv>
-hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t blocks) {
+hipError_t launch_chunk_prep(hipStream_t stream, const GdnParams &p, uint32_t max_chunks) {
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_kernel<Conv>,
+        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_prep_kernel<Conv>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)sizeof(ChunkLds));
+                                                 (int)sizeof(PrepLds));
         if (e != hipSuccess) return e;
         configured = true;
     }
-    SR_LAUNCH("gdn_chunk_kernel", gdn_chunk_kernel<Conv>, dim3(blocks), dim3(kChunkThreads),
-              sizeof(ChunkLds), stream, p);
+    SR_LAUNCH("gdn_chunk_prep_kernel", gdn_chunk_prep_kernel<Conv>,
+              dim3(p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads), sizeof(PrepLds), stream,
+              p);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t max_chunks) {
+    const hipError_t e = p.conv_k == 4 ? launch_chunk_prep<ConvK<4>>(stream, p, max_chunks)
+                                       : launch_chunk_prep<ConvChan>(stream, p, max_chunks);
+    if (e != hipSuccess) return e;
+    const uint32_t pairs = p.nseq * p.value_heads;
+    const uint32_t xcd_map = pairs % 8 == 0 ? 1u : 0u;
+    static bool configured = false;
+    if (!configured) {
+        const hipError_t e2 = hipFuncSetAttribute((const void *)gdn_chunk_scan_kernel,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  (int)sizeof(ScanLds));
+        if (e2 != hipSuccess) return e2;
+        configured = true;
+    }
+    SR_LAUNCH("gdn_chunk_scan_kernel", gdn_chunk_scan_kernel, dim3(pairs * (kHeadDv / kVs)),
+              dim3(kScanThreads), sizeof(ScanLds), stream, p, xcd_map);
     return hipGetLastError();
 }
 
@@ -1252,24 +1401,46 @@ __global__ void __launch_bounds__(256) gdn_norm_gate_kernel(const NormParams p) 
     }
 }
 
+// Which kernels a call takes.  Decode-sized calls (at most kHeadKernelRows
+// rows per sequence) run one workgroup per (sequence, value head) with the
+// norm and gate fused, and so do KEEP_ROWS calls (records of every row).
+// Longer calls with Dv = 128 take the chunked MFMA form, which reads the qkv
+// rows in 16-byte segments; the rest the token-serial row-block kernel.
+enum class GdnRoute { kHead, kChunk, kDelta };
+
+GdnRoute gdn_route(const safetyraise_kernel_gdn_pool *pool, const GdnSeq *seqs, int nseq,
+                   bool keep, bool qkv_aligned) {
+    uint32_t max_rows = 0;
+    for (int i = 0; i < nseq; ++i) max_rows = seqs[i].rows > max_rows ? seqs[i].rows : max_rows;
+    if (pool->value_dim == kHeadDv && (max_rows <= kHeadKernelRows || keep)) return GdnRoute::kHead;
+    if (pool->value_dim == kHeadDv && qkv_aligned) return GdnRoute::kChunk;
+    return GdnRoute::kDelta;
+}
+
 }  // namespace
+
+size_t gdn_chunk_rec_bytes(const safetyraise_kernel_gdn_pool *pool, const GdnSeq *seqs, int nseq,
+                           bool keep, bool qkv_aligned) {
+    if (gdn_route(pool, seqs, nseq, keep, qkv_aligned) != GdnRoute::kChunk) return 0;
+    size_t most = 0;
+    for (int base = 0; base < nseq; base += kMetaPerLaunch) {
+        size_t chunks = 0;
+        for (int i = base; i < nseq && i < base + kMetaPerLaunch; ++i) {
+            chunks += (seqs[i].rows + kCk - 1) / kCk;
+        }
+        most = chunks > most ? chunks : most;
+    }
+    return most * pool->value_heads * kRecFloats * sizeof(float);
+}
 
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs, int nseq,
                       uint32_t total_rows) {
     const auto *pool = g.pool;
-    // decode-sized calls (at most kHeadKernelRows rows per sequence) run one
-    // workgroup per (sequence, value head) with the norm and gate fused;
-    // longer chunks split each head's state rows over workgroups.  KEEP_ROWS
-    // calls (records of every row) always take the token-serial head kernel.
-    uint32_t max_rows = 0;
-    for (int i = 0; i < nseq; ++i) max_rows = seqs[i].rows > max_rows ? seqs[i].rows : max_rows;
     if (g.keep && pool->value_dim != kHeadDv) return hipErrorInvalidValue;
-    const bool head_kernel =
-        pool->value_dim == kHeadDv && (max_rows <= kHeadKernelRows || g.keep);
-    // longer calls with Dv = 128 take the chunked MFMA form (which reads the
-    // qkv rows in 16-byte segments)
-    const bool chunk_kernel = pool->value_dim == kHeadDv && !head_kernel &&
-                              ((uintptr_t)g.qkv & 15) == 0;
+    const GdnRoute route = gdn_route(pool, seqs, nseq, g.keep, ((uintptr_t)g.qkv & 15) == 0);
+    const bool head_kernel = route == GdnRoute::kHead;
+    const bool chunk_kernel = route == GdnRoute::kChunk;
+    if (chunk_kernel && g.chunk_rec == nullptr) return hipErrorInvalidValue;
     for (int base = 0; base < nseq; base += kMetaPerLaunch) {
         const int n = (nseq - base) < kMetaPerLaunch ? (nseq - base) : kMetaPerLaunch;
         GdnParams p;
@@ -1293,9 +1464,14 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs
         p.max_slots = pool->max_sequences;
         p.bf16_in = g.bf16_in ? 1 : 0;
         p.nseq = (uint32_t)n;
+        p.chunk_rec = g.chunk_rec;
+        uint32_t chunks = 0, max_chunks = 0;
         for (int i = 0; i < n; ++i) {
             const GdnSeq &q = seqs[base + i];
-            p.meta[i] = GdnMeta{q.slot, q.rows, q.row0, q.parity, q.state_in, q.state_out};
+            p.meta[i] = GdnMeta{q.slot, q.rows, q.row0, q.parity, q.state_in, q.state_out, chunks};
+            const uint32_t nc = (q.rows + kCk - 1) / kCk;
+            chunks += nc;
+            max_chunks = nc > max_chunks ? nc : max_chunks;
         }
         if (head_kernel) {
             const dim3 grid(pool->value_heads, (uint32_t)n);
@@ -1307,9 +1483,7 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs
                           dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
             }
         } else if (chunk_kernel) {
-            const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kVs);
-            const hipError_t e = p.conv_k == 4 ? launch_chunk<ConvK<4>>(stream, p, blocks)
-                                               : launch_chunk<ConvChan>(stream, p, blocks);
+            const hipError_t e = launch_chunk(stream, p, max_chunks);
             if (e != hipSuccess) return e;
         } else {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kRows);

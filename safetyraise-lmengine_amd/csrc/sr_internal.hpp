@@ -316,6 +316,8 @@ struct GdnLaunch {
     bool keep = false;
     float *records = nullptr;
     uint32_t rec_stride = 0, keep_rows = 0;
+    // chunked prefill: gdn_chunk_rec_bytes(...) bytes of per-chunk records
+    float *chunk_rec = nullptr;
 };
 
 // One sequence of a GDN launch: pool slot, its rows in the call, the
@@ -351,6 +353,11 @@ hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint
                          int num_cus);
 
 // Conv + delta rule over every row of every sequence, then RMSNorm * silu(z).
+// Calls that take the chunked form need g.chunk_rec with
+// gdn_chunk_rec_bytes(...) bytes (0 for other calls; qkv_aligned: the qkv
+// rows the kernels read start 16-byte aligned).
+size_t gdn_chunk_rec_bytes(const safetyraise_kernel_gdn_pool *pool, const GdnSeq *seqs, int nseq,
+                           bool keep, bool qkv_aligned);
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs, int nseq,
                       uint32_t total_rows);
 uint32_t gdn_key_dim();
