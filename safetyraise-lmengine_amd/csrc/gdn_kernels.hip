@@ -638,6 +638,23 @@ __device__ __forceinline__ float fast_silu(float x) {
     return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
+// The value head of grid slot x (0 <= x < Hv) in the chunked kernels.  The
+// dispatcher places workgroup i on XCD i % 8; with key_heads a multiple of 8
+// the slots are ordered so that every value head of a key head lands on one
+// XCD (key head (x % 8) + 8 (slot / groups), slot = x / 8), where the value
+// heads share the key head's q/k rows and their records in its L2.
+__device__ __forceinline__ uint32_t head_of_slot(uint32_t x, uint32_t key_heads, uint32_t groups) {
+    if (key_heads % 8 != 0) return x;
+    const uint32_t slot = x >> 3;
+    return ((x & 7) + 8 * (slot / groups)) * groups + slot % groups;
+}
+
+// e^x with the hardware exp2 (e^{-inf} = 0); for the chunked form's decay
+// factors, held to the f32 tolerance like fast_silu
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(1.4426950408889634f * x);
+}
+
 // One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.
 constexpr int kRecQe = 0;                      // [kCk][kDk]     Qe
 constexpr int kRecWn = kRecQe + kCk * kDk;     // [kCk][kDk]     -W
@@ -665,6 +682,7 @@ struct PrepLds {
     float su[kCk];            //   beta_j (U)
     float ss[kCk];            //   e^{g_C - g_j} / |k_j| (Ks; g_C: last row)
     float qs[kCk];            // Qe's row scales e^{g_t} / |q_t|
+    f32x4 part[2][64];        // second k-halves of the q.k tiles (1, 0) and (1, 1)
     float xin[kPre + kCk][kPin];  // raw inputs: kPre rows before the chunk, then its rows
 };
 
@@ -783,7 +801,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     const int r16 = lane & 15;
     const int sl = lane >> 4;
 
-    const uint32_t h = blockIdx.x;
+    const uint32_t h = head_of_slot(blockIdx.x, p.key_heads, p.value_heads / p.key_heads);
     const uint32_t c = blockIdx.y;
     const GdnMeta m = p.meta[blockIdx.z];
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
@@ -969,29 +987,37 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         sq = sum16(sq);
         sk = sum16(sk);
         if (part == 0) {
-            const float rq = 1.0f / sqrtf(sq + 1e-6f);
+            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
+            const float gt = L.g[t], bt = L.beta[t];
             L.rq[t] = rq;
-            L.rk[t] = 1.0f / sqrtf(sk + 1e-6f);
-            L.qs[t] = rq * expf(L.g[t]);
+            L.rk[t] = rk;
+            L.qs[t] = rq * fast_exp(gt);
+            // column scales of T: W uses beta_j e^{g_j} / |k_j|, U beta_j,
+            // Ks e^{g_C - g_j} / |k_j| (g_C: the last row's g)
+            L.sw[t] = bt * fast_exp(gt) * rk;
+            L.su[t] = bt;
+            L.ss[t] = fast_exp(L.g[kCk - 1] - gt) * rk;
         }
     }
     __syncthreads();
-    // ---- P1: the q.k and k.k tiles on or below the diagonal, one per wave:
-    //      waves 0..2 k.k tiles (0,0), (1,0), (1,1) -> A; waves 3..5 the same
-    //      q.k tiles -> Pm (wave 3 also writes Pm's zero tile (0, 1)); waves
-    //      6 and 7 write Qe = diag(e^{g_t} / |q_t|) Q.
-    if (wave < 6) {
-        const int tile = wave % 3;
-        const int tr = tile == 0 ? 0 : 1, tc = tile == 2 ? 1 : 0;
-        const bool is_kk = wave < 3;
-        const float *arow = is_kk ? &L.k[16 * tr][0] : &L.q[16 * tr][0];
-        f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            constexpr int NH = kDk / 32;
+    // ---- P1: the q.k and k.k tiles on or below the diagonal.  Waves 0..2
+    //      k.k tiles (0,0), (1,0), (1,1) -> A; wave 3 the q.k tile (0,0) -> Pm
+    //      (and Pm's zero tile (0,1)); waves 4..7 halves over k of the q.k
+    //      tiles (1,0) (waves 4, 6) and (1,1) (waves 5, 7), the second halves
+    //      handed over in LDS, so every SIMD runs 48 MFMAs.  Waves 4..7 then
+    //      write Qe and Ks.
+    f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
+    const int p1_tile = wave < 3 ? wave : wave == 3 ? 0 : 1 + (wave & 1);
+    const int p1_tr = p1_tile == 0 ? 0 : 1, p1_tc = p1_tile == 2 ? 1 : 0;
+    {
+        const float *arow = wave < 3 ? &L.k[16 * p1_tr][0] : &L.q[16 * p1_tr][0];
+        constexpr int NH = kDk / 32;
+        // k range: both halves (waves 0..3), the first (4, 5) or second (6, 7)
+        const int h0 = wave < 6 ? 0 : 1, h1 = wave < 4 ? 2 : h0 + 1;
+        for (int half = h0; half < h1; ++half) {
             Ops<NH> xa, kb;
             load_ops(xa, arow + NH * 16 * half, kPr, lane);
-            load_ops(kb, &L.k[16 * tc][NH * 16 * half], kPr, lane);
+            load_ops(kb, &L.k[16 * p1_tc][NH * 16 * half], kPr, lane);
 #pragma unroll
             for (int st = 0; st < NH; ++st) {
                 acc = mfma4(xa.v[st].x, kb.v[st].x, acc);
@@ -1000,37 +1026,46 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
                 acc2 = mfma4(xa.v[st].w, kb.v[st].w, acc2);
             }
         }
-        const int j = 16 * tc + r16;
+        acc += acc2;
+    }
+    if (wave < 4) {
+        const int j = 16 * p1_tc + r16;
         const float gj = L.g[j], rkj = L.rk[j];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int t = 16 * tr + 4 * sl + i;
-            const float gt = L.g[t];
-            const float e = expf(j <= t ? gt - gj : -INFINITY);
-            const float x = acc[i] + acc2[i];
-            if (is_kk) {
-                L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * x : 0.0f;
+            const int t = 16 * p1_tr + 4 * sl + i;
+            const float e = j <= t ? fast_exp(L.g[t] - gj) : 0.0f;
+            if (wave < 3) {
+                L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * acc[i] : 0.0f;
             } else {
-                rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * x;
+                rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
+                rec[kRecPm + t * kCk + 16 + r16] = 0.0f;
             }
         }
-        if (wave == 3) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) rec[kRecPm + (4 * sl + i) * kCk + 16 + r16] = 0.0f;
-        }
     } else {
+        if (wave >= 6) L.part[wave & 1][lane] = acc;
+        const int u = tid - 4 * 64;  // 0..255
 #pragma unroll
-        for (int n = 0; n < 8; ++n) {
-            const int e = tid - 6 * 64 + n * 128;
+        for (int n = 0; n < 4; ++n) {
+            // Qe = diag(e^{g_t} / |q_t|) Q
+            const int e = u + n * 256;
             const int t = e >> 5, d = 4 * (e & 31);
             *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.q[t][d] * L.qs[t];
+        }
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+            // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
+            const int e = u + n * 256;
+            const int d = e >> 3, j = 4 * (e & 7);
+            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
+                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
         }
     }
     __syncthreads();
     // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
     //      blocks by forward substitution (lane j: column j), storing T and
-    //      its transpose; wave 2 clears the upper-right block and wave 3
-    //      computes the column scales and e^{g_C}.
+    //      its transpose; wave 2 clears the upper-right block, wave 3 writes
+    //      e^{g_C}, waves 4 and 5 finish their Pm tiles.
     if (wave < 2) {
         const int b0 = 16 * wave;
         const int j = r16;
@@ -1060,16 +1095,22 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         }
     } else if (wave == 2) {
         for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
-    } else if (wave == 3 && lane < kCk) {
-        const float gj = L.g[lane], rkj = L.rk[lane];
-        L.sw[lane] = L.beta[lane] * expf(gj) * rkj;
-        L.su[lane] = L.beta[lane];
-        L.ss[lane] = expf(L.g[kCk - 1] - gj) * rkj;
+    } else if (wave == 3) {
         if (lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
+    } else if (wave < 6) {
+        acc += L.part[wave & 1][lane];
+        const int j = 16 * p1_tc + r16;
+        const float gj = L.g[j], rkj = L.rk[j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * p1_tr + 4 * sl + i;
+            const float e = j <= t ? fast_exp(L.g[t] - gj) : 0.0f;
+            rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
+        }
     }
     __syncthreads();
     //      T21 = -T22 A21 T11 (wave 0): M = A21 T11 with B = T11^T rows, M^T
-    //      through LDS, then T21 = -T22 M.  Waves 1..7 meanwhile write Ks.
+    //      through LDS, then T21 = -T22 M.
     if (wave == 0) {
         Ops<1> a21, t11t;
         load_ops(a21, &L.a[16][0], kPc, lane);
@@ -1085,13 +1126,6 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         mma(t21, t22, mtr);
 #pragma unroll
         for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
-    } else {
-        // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
-        for (int e = tid - 64; e < kDk * kCk / 4; e += kPrepThreads - 64) {
-            const int d = e >> 3, j = 4 * (e & 7);
-            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
-                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
-        }
     }
     __syncthreads();
     // ---- P3: W = T diag(sw) K (stored negated) and U = T diag(su) V; wave w
@@ -1166,7 +1200,7 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
         vq = b % nq;
         pair = b / nq;
     }
-    const uint32_t h = pair % p.value_heads;
+    const uint32_t h = head_of_slot(pair % p.value_heads, p.key_heads, p.value_heads / p.key_heads);
     const GdnMeta m = p.meta[pair / p.value_heads];
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
     const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
@@ -1348,6 +1382,7 @@ struct NormParams {
     uint32_t value_heads, value_dim, rows;
     float eps;
     int bf16_in;
+    int pairs;          // value_dim 128 and z, norm, out aligned for 2-element accesses
 };
 
 // One wave per (row, value head): rms_norm without offset (math.rs:28-50),
@@ -1357,6 +1392,26 @@ __global__ void __launch_bounds__(256) gdn_norm_gate_kernel(const NormParams p) 
     const int lane = threadIdx.x & 63;
     if (wid >= p.rows * p.value_heads) return;
     const size_t base = (size_t)wid * p.value_dim;
+    if (p.pairs != 0) {
+        // two adjacent dims per lane: one 8-byte load per input
+        const uint32_t d = 2 * (uint32_t)lane;
+        const float2 x = *(const float2 *)(p.raw + base + d);
+        const float2 nw = *(const float2 *)(p.norm + d);
+        float2 zz;
+        if (p.bf16_in != 0) {
+            const uint32_t zb = *(const uint32_t *)((const uint16_t *)p.z + base + d);
+            zz = float2{__uint_as_float(zb << 16), __uint_as_float(zb & 0xffff0000u)};
+        } else {
+            zz = *(const float2 *)((const float *)p.z + base + d);
+        }
+        const float ss = sum64(x.x * x.x + x.y * x.y);
+        const float variance = ss / 128.0f;
+        if (!isfinite(variance) && lane == 0) atomicOr(p.err_word, kErrNonFiniteVariance);
+        const float inv = 1.0f / sqrtf(variance + p.eps);
+        *(float2 *)(p.out + base + d) = float2{x.x * inv * nw.x * (zz.x * ref_sigmoid(zz.x)),
+                                               x.y * inv * nw.y * (zz.y * ref_sigmoid(zz.y))};
+        return;
+    }
     if (p.value_dim <= 4 * 64) {
         // every input of the row (raw, z, weights) is requested before the
         // reduction, so the kernel waits for one memory round trip, not two;
@@ -1504,6 +1559,9 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs
     q.rows = total_rows;
     q.eps = g.eps;
     q.bf16_in = g.bf16_in ? 1 : 0;
+    const uintptr_t zmask = g.bf16_in ? 3 : 7;
+    q.pairs = pool->value_dim == 128 && ((uintptr_t)g.z & zmask) == 0 &&
+              (((uintptr_t)g.norm | (uintptr_t)g.out) & 7) == 0;
     const uint32_t waves = total_rows * pool->value_heads;
     SR_LAUNCH("gdn_norm_gate_kernel", gdn_norm_gate_kernel, dim3((waves + 3) / 4), dim3(256), 0,
               stream, q);

@@ -267,3 +267,38 @@ def test_gdn_chunked_equals_token_serial_and_bf16_device(pkg, backend, rng):
     close(out.cpu().numpy(), exp, what="bf16 device inputs")
     close(pool.read(c)[0], m, what="bf16 state")
     pool.destroy()
+
+
+def test_gdn_device_views_at_odd_offsets(pkg, backend, rng):
+    # device z, norm weights and output as views one element into their
+    # buffers (4-byte but not 8-byte aligned), f32 and bf16 z: the norm/gate
+    # kernel's two-dims-per-lane path needs 8-byte alignment and must fall
+    # back to the scalar path here; prefill- and decode-sized calls
+    import torch
+    L = Layer(rng, 16, 32)
+    pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 2)
+    for rows, bf16 in ((40, False), (40, True), (3, False)):
+        s = pool.open()
+        m, h = seeded_state(rng, L)
+        pool.write(s, m, h)
+        qkv, z, av, bv = L.inputs(rng, rows)
+        if bf16:
+            qkv, z, av, bv = (O.bf16_round(t) for t in (qkv, z, av, bv))
+        exp = oracle_rows(L, (qkv, z, av, bv), m, h)
+        dt = torch.bfloat16 if bf16 else torch.float32
+
+        def odd(t, dtype):
+            flat = torch.from_numpy(np.ascontiguousarray(t).ravel()).to(dtype)
+            buf = torch.zeros(flat.numel() + 1, dtype=dtype, device="cuda")
+            buf[1:] = flat.cuda()
+            return buf[1:].view(t.shape)
+
+        dev = [torch.from_numpy(qkv).to(dt).cuda(), odd(z, dt),
+               torch.from_numpy(av).to(dt).cuda(), torch.from_numpy(bv).to(dt).cuda()]
+        w = [torch.from_numpy(t).cuda() for t in (L.a_log, L.dt_bias, L.conv)] + [odd(L.norm, torch.float32)]
+        out = odd(np.zeros((rows, L.hv * L.dv), np.float32), torch.float32)
+        pkg.gdn_forward(backend, pool, [s], [rows], *dev, *w, out, eps=1e-6)
+        close(out.cpu().numpy(), exp, what=f"rows {rows} bf16 {bf16}")
+        close(pool.read(s)[0], m, what=f"state rows {rows} bf16 {bf16}")
+        pool.close(s)
+    pool.destroy()
