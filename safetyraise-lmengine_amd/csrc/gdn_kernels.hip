@@ -371,14 +371,21 @@ __global__ void __launch_bounds__(NTH) gdn_head_kernel(const GdnParams p, const 
     }
     // inputs of a row: qkv channels, z of this head (dims lane and lane + 64,
     // used by wave 0), a and b
+    // a and b are the same for every lane; read through a per-lane offset the
+    // compiler cannot fold (zero), they stay in vector registers.  As
+    // wave-uniform values they were moved to scalar registers right after
+    // the next row's loads, and that move waited for every load in flight,
+    // the whole state included.
+    uint32_t vzero = 0;
+    asm volatile("" : "+v"(vzero));
     float x0 = 0.0f, x1 = 0.0f, z0 = 0.0f, z1 = 0.0f, av = 0.0f, bv = 0.0f;
     auto load_row = [&](size_t row) {
         x0 = load_act_nb(a.qkv, row * a.channels + ch0, bf16_in);
         if constexpr (kTwo) x1 = load_act_nb(a.qkv, row * a.channels + ch1, bf16_in);
         z0 = load_act_nb(a.z, row * width + h * kHeadDv + lane, bf16_in);
         z1 = load_act_nb(a.z, row * width + h * kHeadDv + lane + 64, bf16_in);
-        av = load_act_nb(a.a, row * a.value_heads + h, bf16_in);
-        bv = load_act_nb(a.b, row * a.value_heads + h, bf16_in);
+        av = load_act_nb(a.a, row * a.value_heads + h + vzero, bf16_in);
+        bv = load_act_nb(a.b, row * a.value_heads + h + vzero, bf16_in);
     };
     load_row(m.row0);
     // state rows v = (NTH/16) i + group, dims [4 l16, 4 l16 + 4) and

@@ -302,3 +302,23 @@ def test_gdn_device_views_at_odd_offsets(pkg, backend, rng):
         close(pool.read(s)[0], m, what=f"state rows {rows} bf16 {bf16}")
         pool.close(s)
     pool.destroy()
+
+
+def test_gdn_chunked_form_more_than_64_sequences(pkg, backend, rng):
+    # 70 sequences in one call with more than 8 rows somewhere, so every one
+    # takes the chunked form: two launch batches (64 + 6 sequences) that
+    # reuse one set of chunk records; 1..40 rows each (one or two chunks,
+    # full and partial), seeded states
+    L = Layer(rng, 2, 4)
+    pool = pkg.GdnState(backend, 2, 4, 128, 128, 4, 70)
+    seqs, refs = [], []
+    for _ in range(70):
+        s = pool.open()
+        m, h = seeded_state(rng, L)
+        pool.write(s, m, h)
+        seqs.append(s)
+        refs.append((m.copy(), h.copy()))
+    rows = [int(r) for r in rng.integers(1, 41, size=70)]
+    rows[3] = 40
+    run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, "70 sequences")
+    pool.destroy()
