@@ -929,9 +929,13 @@ def bench_linear_prefill(args, torch, pkg, steps, warmup, rows=2048):
     ms = t0.elapsed_time(t1) / steps
     flops = [2 * rows * o * i for o, i in LINEAR_SHAPES]
     tflops = sum(flops) / (ms * 1e-3) / 1e12
-    gemm_us = kernels["linear_gemm_kernel"]["us"]
-    # the roofline: the gate/up shape, the MFMA work of one call (3 passes)
-    # over the average tiled-kernel launch weighted as the calls' FLOPs are
+    # the tiled products: linear_gemm_wide_kernel for calls with many
+    # outputs, linear_gemm_kernel for the others; their mean launch over all
+    # calls, weighted by the share of calls each takes
+    tiled = [kernels[k] for k in ("linear_gemm_wide_kernel", "linear_gemm_kernel") if k in kernels]
+    gemm_us = sum(k["per_call"] * k["us"] for k in tiled) / sum(k["per_call"] for k in tiled)
+    # the roofline: the MFMA work of one call (3 passes) over the mean
+    # tiled-kernel launch, the calls' FLOPs averaged the same way
     launch_flops = sum(flops) / len(flops)
     mfma_tf = 3 * launch_flops / (gemm_us * 1e-6) / 1e12
     result = {
@@ -944,8 +948,9 @@ def bench_linear_prefill(args, torch, pkg, steps, warmup, rows=2048):
             "bound": "mfma", "achieved": round(mfma_tf, 2), "peak": MFMA_BF16_PEAK_TFS,
             "unit": "TFLOP/s", "frac": round(mfma_tf / MFMA_BF16_PEAK_TFS, 4),
             "traffic": None,
-            "kernel": "linear_gemm_kernel (all seven calls; achieved = 3 bf16 MFMA passes per "
-                      "exact product, the calls' mean FLOPs over the mean launch)",
+            "kernel": "linear_gemm_wide_kernel + linear_gemm_kernel (all seven calls; achieved = "
+                      "3 bf16 MFMA passes per exact product, the calls' mean FLOPs over the mean "
+                      "launch)",
             "launch_us_mean": round(float(gemm_us), 2),
             "flops_per_launch": int(3 * launch_flops),
             "exact_product_tflops_per_launch": round(launch_flops / (gemm_us * 1e-6) / 1e12, 2),

@@ -151,12 +151,14 @@ def test_multi_tile_plans_with_partial_blocks(backend, rng, rows, cols, out):
     assert np.array_equal(backend.linear(wi, xi, BF16), O.linear(xi, wi, BF16))
 
 
-@pytest.mark.parametrize("rows,cols,out", [(256, 64, 8192), (130, 512, 16000), (300, 192, 6000)])
+@pytest.mark.parametrize("rows,cols,out", [(256, 64, 8192), (130, 512, 16000), (300, 192, 6000),
+                                           (2048, 128, 1024)])
 def test_prefill_sized_calls_take_the_tiled_product(backend, rng, rows, cols, out):
     # 64+ rows with K a multiple of 64 on a bf16 weight, with at least 128
     # output tiles of 128 x 128, take the tiled product (x split once per
-    # workgroup through LDS): one 64-k stage, an even and an odd number of
-    # stages, rows and outputs past the last whole tile
+    # workgroup through LDS): calls with 2048+ outputs the 4-wave form, the
+    # 1024-output call the 8-wave one; one, three and eight stage pairs, rows
+    # and outputs past the last whole tile; random and integer inputs
     x = (2 * rng.standard_normal((rows, cols))).astype(np.float32)
     bits = weight_bits(rng.standard_normal((out, cols)), BF16)
     got = backend.linear(bits, x, BF16)
@@ -164,6 +166,9 @@ def test_prefill_sized_calls_take_the_tiled_product(backend, rng, rows, cols, ou
     mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, BF16)).T
     bad = np.abs(got - ref) > 1e-5 * mag + 1e-4 * np.abs(ref)
     assert not bad.any(), (rows, cols, out, np.abs(got - ref).max())
+    xi = rng.integers(-8, 9, size=(rows, cols)).astype(np.float32)
+    wi = weight_bits(rng.integers(-8, 9, size=(out, cols)).astype(np.float32), BF16)
+    assert np.array_equal(backend.linear(wi, xi, BF16), O.linear(xi, wi, BF16))
 
 
 def test_prefill_sized_integer_inputs_bit_exact(backend, rng):
