@@ -792,7 +792,7 @@ constexpr uint32_t kMaxRows = 65535u * kLinTile;  // grid y limit of one row-til
 // row-tile kernel's weight stream is faster).  Calls above kMaxRows rows run
 // as row blocks without scratch.
 bool gemm_applies(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, int num_cus) {
-    if (dtype != SAFETYRAISE_KERNEL_DTYPE_BF16 || M < kGemmMinRows || M > kMaxRows ||
+    if (dtype != SAFETYRAISE_KERNEL_DTYPE_BF16 || M < kGemmMinRows || M > kMaxRows || K == 0 ||
         K % kGemmK != 0) {
         return false;
     }
@@ -811,10 +811,24 @@ size_t linear_scratch_bytes(uint32_t M, uint32_t N, uint32_t K, uint32_t dtype, 
     return s > 1 ? (size_t)s * M * N * sizeof(float) : 0;
 }
 
+// y = 0 for calls with no inputs per output (K = 0): the sum over an empty
+// row, as the reference's loop leaves it (a kernel, not a memset, so that a
+// captured stream records no memset node)
+__global__ __launch_bounds__(256) void linear_zero_kernel(float *y, uint64_t count) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < count) y[i] = 0.0f;
+}
+
 hipError_t launch_linear(hipStream_t stream, const float *x, const void *w, uint32_t dtype,
                          float *y, uint32_t M, uint32_t N, uint32_t K, float *scratch,
                          int num_cus) {
     if (M == 0 || N == 0) return hipSuccess;
+    if (K == 0) {
+        const uint64_t count = (uint64_t)M * N;
+        SR_LAUNCH("linear_zero_kernel", linear_zero_kernel, dim3((uint32_t)((count + 255) / 256)),
+                  dim3(256), 0, stream, y, count);
+        return hipGetLastError();
+    }
     if (M > kMaxRows) {
         // equal blocks of rows, one launch each: every block has at least
         // kMaxRows / 2 rows, so enough tiles that none splits K and the

@@ -253,3 +253,30 @@ def test_rows_beyond_one_launch_grid(backend, rng):
     w = rng.integers(-4, 5, size=(3, 8)).astype(np.float32)
     got = backend.linear(w, x, F32)
     assert np.array_equal(got, O.linear(x, w, F32))
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_weights_without_columns_give_zeros(backend, rng, torch_mod, dtype):
+    # K = 0: every output is the empty sum, 0 (the reference's loop over no
+    # inputs); rows below and above the tiled product's minimum, device
+    # outputs prefilled with NaN, and a host call after a call that left
+    # non-zero values in the plugin's output buffer
+    torch = torch_mod
+    for rows, out in ((5, 300), (100, 3000)):
+        empty = weight_bits(np.zeros((out, 0)), dtype)
+        prepared = backend.create_weight(empty, dtype)
+        try:
+            x = np.zeros((rows, 0), np.float32)
+            dy = torch.full((rows, out), float("nan"), device="cuda")
+            dx = torch.zeros((rows, 1), device="cuda")  # any valid pointer; no input is read
+            backend.check(backend.lib.safetyraise_kernel_linear_device(
+                backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), rows, 0,
+                C.c_void_p(dy.data_ptr()), rows, out), "linear_device")
+            backend.synchronize()
+            assert np.array_equal(dy.cpu().numpy(), np.zeros((rows, out), np.float32))
+            full = weight_bits(rng.standard_normal((out, 64)), dtype)
+            backend.linear(full, rng.standard_normal((rows, 64)).astype(np.float32), dtype)
+            assert np.array_equal(backend.linear(prepared, x), np.zeros((rows, out), np.float32))
+            assert np.array_equal(O.linear(x, empty, dtype), np.zeros((rows, out), np.float32))
+        finally:
+            prepared.destroy()
