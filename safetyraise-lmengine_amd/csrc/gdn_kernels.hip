@@ -671,13 +671,15 @@ constexpr int kRecPm = kRecKs + kDk * kCk;     // [kCk][kCk]     Pm
 constexpr int kRecEc = kRecPm + kCk * kCk;     // e^{g_C}
 constexpr int kRecFloats = kRecEc + 64;        // a 256-byte multiple
 constexpr int kPre = kMaxK - 1;                // raw input rows staged before a chunk
-constexpr int kPin = 2 * kDk + kHeadDv;        // raw input channels of a (chunk, value head)
+constexpr int kPin = 2 * kDk;                  // raw input channels a prep workgroup stages
 
 struct PrepLds {
-    float q[kCk][kPr];        // conv(q) rows t
+    union {
+        float q[kCk][kPr];       // role 0: conv(q) rows t
+        float vc[kHeadDv][kPc];  // role 1: conv(v) transposed: [v][t]
+    } qv;
     float k[kCk][kPr];        // conv(k) rows t
     float kc[kDk][kPc];       // conv(k) transposed: [d][t]
-    float vc[kHeadDv][kPc];   // conv(v) transposed: [v][t]
     float a[kCk][kPc];        // A (strictly lower)
     float t[kCk][kPc];        // T = (I + A)^-1
     float tt[kCk][kPc];       // T11^T, then M^T (P2 scratch)
@@ -808,7 +810,12 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     const int r16 = lane & 15;
     const int sl = lane >> 4;
 
-    const uint32_t h = head_of_slot(blockIdx.x, p.key_heads, p.value_heads / p.key_heads);
+    // two workgroups per (sequence, chunk, value head): role 0 (grid slots
+    // 0 .. Hv-1) stages q and k and writes Qe, Pm and -W; role 1 stages k and
+    // v and writes U, Ks and e^{g_C}.  Both form A from k.k and invert it.
+    const bool role_w = blockIdx.x < p.value_heads;  // uniform
+    const uint32_t h = head_of_slot(role_w ? blockIdx.x : blockIdx.x - p.value_heads, p.key_heads,
+                                    p.value_heads / p.key_heads);
     const uint32_t c = blockIdx.y;
     const GdnMeta m = p.meta[blockIdx.z];
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
@@ -824,22 +831,23 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     constexpr int KC = Conv::kK;  // 0: run-time kernel size
     const int Kr = KC ? KC : (int)p.conv_k;
 
-    // conv work of this thread (the row ranges are wave-uniform): q/k channel
-    // qc (q dim qc < 128, else k dim qc - 128) over rows 16 qhalf .. + 15, and
-    // v channel vch over rows 8 vquart .. + 7
-    const int qc = tid & (2 * kDk - 1);
-    const int qhalf = tid >> 8;
-    const int vch = tid & (kHeadDv - 1);
-    const int vquart = tid >> 7;
-    const uint32_t ch0 = qc < kDk ? kh * kDk + qc : key_width + kh * kDk + (qc - kDk);
-    const uint32_t ch1 = 2 * key_width + h * kHeadDv + vch;
+    // the role's 256 staged channels: lc < 128 the first range (q for role
+    // 0, k for role 1), the rest the second (k, v); global channel of lc
+    auto chan = [&](int lc) -> uint32_t {
+        if (role_w) return lc < kDk ? kh * kDk + lc : key_width + kh * kDk + (lc - kDk);
+        return lc < kDk ? key_width + kh * kDk + lc : 2 * key_width + h * kHeadDv + (lc - kDk);
+    };
+    // conv work of this thread: channel lc over rows 16 half .. + 15 (the
+    // half is wave-uniform)
+    const int lc = tid & (kPin - 1);
+    const int half = tid >> 8;
+    const uint32_t ch = chan(lc);
     const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
     const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
     // weights and the stored history (used by the rows that start the call;
     // the others take the K-1 inputs before them from the staged rows)
-    Conv cv0, cvv;
-    cv0.load(p.history + (hist_slot + ch0) * K1, p.conv_w + (size_t)ch0 * p.conv_k, p.conv_k);
-    cvv.load(p.history + (hist_slot + ch1) * K1, p.conv_w + (size_t)ch1 * p.conv_k, p.conv_k);
+    Conv cv;
+    cv.load(p.history + (hist_slot + ch) * K1, p.conv_w + (size_t)ch * p.conv_k, p.conv_k);
 
     // decay and write strength inputs first: wave 1 turns them into g and
     // beta while the raw inputs below are in flight
@@ -871,16 +879,13 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     };
     // ---- raw inputs: rows r0 - kPre .. r0 + kCk - 1 of the sequence, clamped
     //      into its rows (clamped copies are never used), in 16-byte segments
-    //      of the three channel ranges, every load in flight together
+    //      of the two channel ranges, every load in flight together
     {
         uint32_t lt = tid;
         pin(lt);
         auto seg_src = [&](int rr, int c0) -> size_t {
-            const uint32_t ch = c0 < kDk ? kh * kDk + c0
-                              : c0 < 2 * kDk ? key_width + kh * kDk + (c0 - kDk)
-                                             : 2 * key_width + h * kHeadDv + (c0 - 2 * kDk);
             const int row = min(max((int)r0 - kPre + rr, 0), (int)m.rows - 1);
-            return ((size_t)m.row0 + row) * p.channels + ch;
+            return ((size_t)m.row0 + row) * p.channels + chan(c0);
         };
         constexpr int R = kPre + kCk;
         if (!bf16_in) {
@@ -924,107 +929,103 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     __syncthreads();
     // ---- causal conv + silu (math.rs:158-187); rows past nv are zero and do
     //      not advance the history
-    if (c > 0 || qhalf == 1) cv0.set_hist(&L.xin[kPre + 16 * qhalf - (Kr - 1)][qc], kPin, p.conv_k);
-    if (c > 0 || vquart > 0) {
-        cvv.set_hist(&L.xin[kPre + 8 * vquart - (Kr - 1)][2 * kDk + vch], kPin, p.conv_k);
-    }
+    if (c > 0 || half == 1) cv.set_hist(&L.xin[kPre + 16 * half - (Kr - 1)][lc], kPin, p.conv_k);
     {
-        const int tb = 16 * qhalf;
+        const int tb = 16 * half;
         float xr[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xr[i] = L.xin[kPre + tb + i][qc];
+        for (int i = 0; i < 16; ++i) xr[i] = L.xin[kPre + tb + i][lc];
         float yr[16];
         if (tb + 16 <= (int)nv) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
+            for (int i = 0; i < 16; ++i) yr[i] = fast_silu(cv.pre(xr[i], p.conv_k));
         } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 yr[i] = 0.0f;
-                if ((uint32_t)(tb + i) < nv) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
+                if ((uint32_t)(tb + i) < nv) yr[i] = fast_silu(cv.pre(xr[i], p.conv_k));
             }
         }
-        if (qc < kDk) {
+        // role 0: q -> q, k -> k and kc; role 1: k -> k and kc, v -> vc
+        const bool is_k = role_w ? lc >= kDk : lc < kDk;  // wave-uniform
+        const int d = lc & (kDk - 1);
+        if (is_k) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) L.q[tb + i][qc] = yr[i];
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) L.k[tb + i][qc - kDk] = yr[i];
+            for (int i = 0; i < 16; ++i) L.k[tb + i][d] = yr[i];
 #pragma unroll
             for (int i = 0; i < 16; i += 4) {
-                *(f32x4 *)&L.kc[qc - kDk][tb + i] = f32x4{yr[i], yr[i + 1], yr[i + 2], yr[i + 3]};
+                *(f32x4 *)&L.kc[d][tb + i] = f32x4{yr[i], yr[i + 1], yr[i + 2], yr[i + 3]};
+            }
+        } else if (role_w) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) L.qv.q[tb + i][d] = yr[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                *(f32x4 *)&L.qv.vc[d][tb + i] = f32x4{yr[i], yr[i + 1], yr[i + 2], yr[i + 3]};
             }
         }
-    }
-    {
-        const int tb = 8 * vquart;
-        float xr[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) xr[i] = L.xin[kPre + tb + i][2 * kDk + vch];
-        float yv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            yv[i] = 0.0f;
-            if ((uint32_t)(tb + i) < nv) yv[i] = fast_silu(cvv.pre(xr[i], p.conv_k));
+        // the history after the call: the last K-1 raw inputs, from the last
+        // chunk, by the half that holds the last row; q/k channels by role 0
+        // of the key head's first value head, v channels by role 1
+        if (c + 1 == nchunks && half == (nv > 16 ? 1 : 0) &&
+            (role_w ? h % groups == 0 : lc >= kDk)) {
+            cv.store(p.history + (hist_next + ch) * K1, p.conv_k);
         }
-        *(f32x4 *)&L.vc[vch][tb] = f32x4{yv[0], yv[1], yv[2], yv[3]};
-        *(f32x4 *)&L.vc[vch][tb + 4] = f32x4{yv[4], yv[5], yv[6], yv[7]};
-    }
-    // the history after the call: the last K-1 raw inputs, from the last
-    // chunk, by the threads whose rows hold the last row (q/k channels only
-    // in the first value head of the key head)
-    if (c + 1 == nchunks) {
-        if (h % groups == 0 && qhalf == (nv > 16 ? 1 : 0)) cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
-        if (vquart == (int)(nv - 1) / 8) cvv.store(p.history + (hist_next + ch1) * K1, p.conv_k);
     }
     __syncthreads();
-    // ---- L2 norms of q and k per row (math.rs:218-219): 16 lanes per row,
-    //      8 dims each, then a reduction over the 16; and Qe's row scale
-    //      e^{g_t} / |q_t|
+    // ---- L2 norms per row (math.rs:218-219): 16 lanes per row, 8 dims each,
+    //      a reduction over the 16; then the row's scales
     {
         const int t = 4 * wave + (lane >> 4), part = lane & 15;
         float sq = 0.0f, sk = 0.0f;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const float4 a4 = *(const float4 *)&L.q[t][8 * part + 4 * i];
             const float4 b4 = *(const float4 *)&L.k[t][8 * part + 4 * i];
-            sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
             sk += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
+            if (role_w) {
+                const float4 a4 = *(const float4 *)&L.qv.q[t][8 * part + 4 * i];
+                sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
+            }
         }
-        sq = sum16(sq);
         sk = sum16(sk);
+        if (role_w) sq = sum16(sq);
         if (part == 0) {
-            const float rq = 1.0f / sqrtf(sq + 1e-6f), rk = 1.0f / sqrtf(sk + 1e-6f);
+            const float rk = 1.0f / sqrtf(sk + 1e-6f);
             const float gt = L.g[t], bt = L.beta[t];
-            L.rq[t] = rq;
             L.rk[t] = rk;
-            L.qs[t] = rq * fast_exp(gt);
-            // column scales of T: W uses beta_j e^{g_j} / |k_j|, U beta_j,
-            // Ks e^{g_C - g_j} / |k_j| (g_C: the last row's g)
-            L.sw[t] = bt * fast_exp(gt) * rk;
-            L.su[t] = bt;
-            L.ss[t] = fast_exp(L.g[kCk - 1] - gt) * rk;
+            if (role_w) {
+                // Qe's row scale e^{g_t} / |q_t|; W's column scale of T,
+                // beta_j e^{g_j} / |k_j|
+                const float rq = 1.0f / sqrtf(sq + 1e-6f);
+                L.rq[t] = rq;
+                L.qs[t] = rq * fast_exp(gt);
+                L.sw[t] = bt * fast_exp(gt) * rk;
+            } else {
+                // U's column scale beta_j; Ks's e^{g_C - g_j} / |k_j|
+                L.su[t] = bt;
+                L.ss[t] = fast_exp(L.g[kCk - 1] - gt) * rk;
+            }
         }
     }
     __syncthreads();
-    // ---- P1: the q.k and k.k tiles on or below the diagonal.  Waves 0..2
-    //      k.k tiles (0,0), (1,0), (1,1) -> A; wave 3 the q.k tile (0,0) -> Pm
-    //      (and Pm's zero tile (0,1)); waves 4..7 halves over k of the q.k
-    //      tiles (1,0) (waves 4, 6) and (1,1) (waves 5, 7), the second halves
-    //      handed over in LDS, so every SIMD runs 48 MFMAs.  Waves 4..7 then
-    //      write Qe and Ks.
+    // ---- P1: the k.k tiles (0,0), (1,0), (1,1) -> A on waves 0..2.  Role 0
+    //      also the q.k tiles: wave 3 (0,0) -> Pm (and Pm's zero tile (0,1)),
+    //      waves 4..7 halves over k of (1,0) (waves 4, 6) and (1,1) (5, 7),
+    //      the second halves handed over in LDS, so every SIMD runs 48 MFMAs;
+    //      waves 4..7 then write Qe.  Role 1: waves 3..7 write Ks.
     f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
     const int p1_tile = wave < 3 ? wave : wave == 3 ? 0 : 1 + (wave & 1);
     const int p1_tr = p1_tile == 0 ? 0 : 1, p1_tc = p1_tile == 2 ? 1 : 0;
-    {
-        const float *arow = wave < 3 ? &L.k[16 * p1_tr][0] : &L.q[16 * p1_tr][0];
+    if (wave < 3 || role_w) {
+        const float *arow = wave < 3 ? &L.k[16 * p1_tr][0] : &L.qv.q[16 * p1_tr][0];
         constexpr int NH = kDk / 32;
         // k range: both halves (waves 0..3), the first (4, 5) or second (6, 7)
         const int h0 = wave < 6 ? 0 : 1, h1 = wave < 4 ? 2 : h0 + 1;
-        for (int half = h0; half < h1; ++half) {
+        for (int hh = h0; hh < h1; ++hh) {
             Ops<NH> xa, kb;
-            load_ops(xa, arow + NH * 16 * half, kPr, lane);
-            load_ops(kb, &L.k[16 * p1_tc][NH * 16 * half], kPr, lane);
+            load_ops(xa, arow + NH * 16 * hh, kPr, lane);
+            load_ops(kb, &L.k[16 * p1_tc][NH * 16 * hh], kPr, lane);
 #pragma unroll
             for (int st = 0; st < NH; ++st) {
                 acc = mfma4(xa.v[st].x, kb.v[st].x, acc);
@@ -1035,7 +1036,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         }
         acc += acc2;
     }
-    if (wave < 4) {
+    if (wave < 3 || (role_w && wave == 3)) {
         const int j = 16 * p1_tc + r16;
         const float gj = L.g[j], rkj = L.rk[j];
 #pragma unroll
@@ -1049,7 +1050,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
                 rec[kRecPm + t * kCk + 16 + r16] = 0.0f;
             }
         }
-    } else {
+    } else if (role_w) {
         if (wave >= 6) L.part[wave & 1][lane] = acc;
         const int u = tid - 4 * 64;  // 0..255
 #pragma unroll
@@ -1057,12 +1058,11 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             // Qe = diag(e^{g_t} / |q_t|) Q
             const int e = u + n * 256;
             const int t = e >> 5, d = 4 * (e & 31);
-            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.q[t][d] * L.qs[t];
+            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.qv.q[t][d] * L.qs[t];
         }
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-            // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
-            const int e = u + n * 256;
+    } else {
+        // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
+        for (int e = tid - 3 * 64; e < kDk * kCk / 4; e += kPrepThreads - 3 * 64) {
             const int d = e >> 3, j = 4 * (e & 7);
             *(f32x4 *)(rec + kRecKs + d * kCk + j) =
                 *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
@@ -1071,8 +1071,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     __syncthreads();
     // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
     //      blocks by forward substitution (lane j: column j), storing T and
-    //      its transpose; wave 2 clears the upper-right block, wave 3 writes
-    //      e^{g_C}, waves 4 and 5 finish their Pm tiles.
+    //      its transpose; wave 2 clears the upper-right block; role 1's wave
+    //      3 writes e^{g_C}; role 0's waves 4 and 5 finish their Pm tiles.
     if (wave < 2) {
         const int b0 = 16 * wave;
         const int j = r16;
@@ -1103,8 +1103,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     } else if (wave == 2) {
         for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
     } else if (wave == 3) {
-        if (lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
-    } else if (wave < 6) {
+        if (!role_w && lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
+    } else if (wave < 6 && role_w) {
         acc += L.part[wave & 1][lane];
         const int j = 16 * p1_tc + r16;
         const float gj = L.g[j], rkj = L.rk[j];
@@ -1135,39 +1135,34 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
     }
     __syncthreads();
-    // ---- P3: W = T diag(sw) K (stored negated) and U = T diag(su) V; wave w
-    //      owns rows 16 (w & 1).. and columns 32 (w >> 1) .. + 31 of both
+    // ---- P3: role 0 W = T diag(sw) K (stored negated), role 1
+    //      U = T diag(su) V; wave w owns rows 16 (w & 1).. and columns
+    //      32 (w >> 1) .. + 31
     {
         const int tr = wave & 1, c0 = 32 * (wave >> 1);
-        Ops<2> tw, tu;
-        load_ops(tw, &L.t[16 * tr][0], kPc, lane);
-        tu = tw;
-        Ops<2> kb2[2], vb2[2];
+        Ops<2> ta;
+        load_ops(ta, &L.t[16 * tr][0], kPc, lane);
+        scale_ops(ta, role_w ? L.sw : L.su, lane);
+        Ops<2> xb[2];
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
-            load_ops(kb2[n], &L.kc[c0 + 16 * n][0], kPc, lane);
-            load_ops(vb2[n], &L.vc[c0 + 16 * n][0], kPc, lane);
+            load_ops(xb[n], role_w ? &L.kc[c0 + 16 * n][0] : &L.qv.vc[c0 + 16 * n][0], kPc, lane);
         }
-        scale_ops(tw, L.sw, lane);
-        scale_ops(tu, L.su, lane);
-        f32x4 w[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
-        f32x4 u[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        f32x4 o[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
         for (int st = 0; st < 2; ++st)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int n = 0; n < 2; ++n) {
-                    w[n] = mfma4(tw.v[st][e], kb2[n].v[st][e], w[n]);
-                    u[n] = mfma4(tu.v[st][e], vb2[n].v[st][e], u[n]);
-                }
+                for (int n = 0; n < 2; ++n) o[n] = mfma4(ta.v[st][e], xb[n].v[st][e], o[n]);
+        float *dst = rec + (role_w ? kRecWn : kRecU);
+        const float sign = role_w ? -1.0f : 1.0f;
 #pragma unroll
         for (int n = 0; n < 2; ++n)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
-                rec[kRecWn + t * kDk + col] = -w[n][i];
-                rec[kRecU + t * kHeadDv + col] = u[n][i];
+                dst[t * kDk + col] = sign * o[n][i];
             }
     }
 }
@@ -1356,7 +1351,7 @@ hipError_t launch_chunk_prep(hipStream_t stream, const GdnParams &p, uint32_t ma
         configured = true;
     }
     SR_LAUNCH("gdn_chunk_prep_kernel", gdn_chunk_prep_kernel<Conv>,
-              dim3(p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads), sizeof(PrepLds), stream,
+              dim3(2 * p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads), sizeof(PrepLds), stream,
               p);
     return hipGetLastError();
 }
