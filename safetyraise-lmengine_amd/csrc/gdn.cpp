@@ -331,6 +331,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_forward(
     char *base = (char *)ctx->staging.ptr;
     g.raw = (float *)base;
     g.chunk_rec = rec_b > 0 ? (float *)(base + rec_off) : nullptr;
+    g.num_cus = ctx->num_cus;
     if (!device) {
         for (auto &r : regions) {
             SR_HIP(ctx, hipMemcpyAsync(base + r.off, r.host, r.bytes, hipMemcpyHostToDevice,

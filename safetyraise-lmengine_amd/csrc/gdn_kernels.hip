@@ -19,6 +19,8 @@
 // another still has to read.
 #include "sr_device.hpp"
 
+#include <type_traits>
+
 namespace sr {
 
 namespace {
@@ -671,29 +673,6 @@ constexpr int kRecPm = kRecKs + kDk * kCk;     // [kCk][kCk]     Pm
 constexpr int kRecEc = kRecPm + kCk * kCk;     // e^{g_C}
 constexpr int kRecFloats = kRecEc + 64;        // a 256-byte multiple
 constexpr int kPre = kMaxK - 1;                // raw input rows staged before a chunk
-constexpr int kPin = 2 * kDk;                  // raw input channels a prep workgroup stages
-
-struct PrepLds {
-    union {
-        float q[kCk][kPr];       // role 0: conv(q) rows t
-        float vc[kHeadDv][kPc];  // role 1: conv(v) transposed: [v][t]
-    } qv;
-    float k[kCk][kPr];        // conv(k) rows t
-    float kc[kDk][kPc];       // conv(k) transposed: [d][t]
-    float a[kCk][kPc];        // A (strictly lower)
-    float t[kCk][kPc];        // T = (I + A)^-1
-    float tt[kCk][kPc];       // T11^T, then M^T (P2 scratch)
-    float g[kCk];             // cumulative log decay
-    float beta[kCk];
-    float rq[kCk];            // 1 / |q_t|
-    float rk[kCk];            // 1 / |k_t|
-    float sw[kCk];            // column scales of T: beta_j e^{g_j} / |k_j| (W)
-    float su[kCk];            //   beta_j (U)
-    float ss[kCk];            //   e^{g_C - g_j} / |k_j| (Ks; g_C: last row)
-    float qs[kCk];            // Qe's row scales e^{g_t} / |q_t|
-    f32x4 part[2][64];        // second k-halves of the q.k tiles (1, 0) and (1, 1)
-    float xin[kPre + kCk][kPin];  // raw inputs: kPre rows before the chunk, then its rows
-};
 
 struct ScanLds {
     float s0[kVs][kPr];  // state slice: rows v, dims d
@@ -799,10 +778,46 @@ __device__ __forceinline__ float pick(const float (&a)[N], int i) {
     return x;
 }
 
-template <class Conv>
+// Prep forms: one workgroup per (sequence, chunk, value head) forming the
+// whole record, or (kSplit) two, one forming -W, Qe and Pm (grid slots
+// 0 .. Hv-1) and the other U, Ks and e^{g_C} (slots Hv .. 2 Hv - 1), both
+// forming A from k.k and inverting it.  Two per record keep every CU busy
+// when a call has few chunks; with many chunks the shared part done twice
+// costs more than it saves.
+template <bool kSplit>
+struct PrepLds {
+    static constexpr int kIn = kSplit ? 2 * kDk : 2 * kDk + kHeadDv;  // staged channels
+    struct Both {
+        float q[kCk][kPr];        // conv(q) rows t
+        float vc[kHeadDv][kPc];   // conv(v) transposed: [v][t]
+    };
+    union One {                   // a split workgroup uses one of them
+        float q[kCk][kPr];
+        float vc[kHeadDv][kPc];
+    };
+    typename std::conditional<kSplit, One, Both>::type qv;
+    float k[kCk][kPr];        // conv(k) rows t
+    float kc[kDk][kPc];       // conv(k) transposed: [d][t]
+    float a[kCk][kPc];        // A (strictly lower)
+    float t[kCk][kPc];        // T = (I + A)^-1
+    float tt[kCk][kPc];       // T11^T, then M^T (P2 scratch)
+    float g[kCk];             // cumulative log decay
+    float beta[kCk];
+    float rq[kCk];            // 1 / |q_t|
+    float rk[kCk];            // 1 / |k_t|
+    float sw[kCk];            // column scales of T: beta_j e^{g_j} / |k_j| (W)
+    float su[kCk];            //   beta_j (U)
+    float ss[kCk];            //   e^{g_C - g_j} / |k_j| (Ks; g_C: last row)
+    float qs[kCk];            // Qe's row scales e^{g_t} / |q_t|
+    f32x4 part[2][64];        // second k-halves of the q.k tiles (1, 0) and (1, 1)
+    float xin[kPre + kCk][kIn];  // raw inputs: kPre rows before the chunk, then its rows
+};
+
+template <class Conv, bool kSplit>
 __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnParams p) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    PrepLds &L = *(PrepLds *)lds_raw;
+    PrepLds<kSplit> &L = *(PrepLds<kSplit> *)lds_raw;
+    constexpr int kIn = PrepLds<kSplit>::kIn;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -810,12 +825,12 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     const int r16 = lane & 15;
     const int sl = lane >> 4;
 
-    // two workgroups per (sequence, chunk, value head): role 0 (grid slots
-    // 0 .. Hv-1) stages q and k and writes Qe, Pm and -W; role 1 stages k and
-    // v and writes U, Ks and e^{g_C}.  Both form A from k.k and invert it.
-    const bool role_w = blockIdx.x < p.value_heads;  // uniform
-    const uint32_t h = head_of_slot(role_w ? blockIdx.x : blockIdx.x - p.value_heads, p.key_heads,
-                                    p.value_heads / p.key_heads);
+    // the record parts this workgroup forms (uniform); grid slot: value
+    // head x, or x + Hv for the U part of a split pair
+    const bool u_only = kSplit && blockIdx.x >= p.value_heads;
+    const bool kW = !u_only, kU = !kSplit || u_only;
+    const uint32_t x = u_only ? blockIdx.x - p.value_heads : blockIdx.x;
+    const uint32_t h = head_of_slot(x, p.key_heads, p.value_heads / p.key_heads);
     const uint32_t c = blockIdx.y;
     const GdnMeta m = p.meta[blockIdx.z];
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
@@ -831,23 +846,31 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     constexpr int KC = Conv::kK;  // 0: run-time kernel size
     const int Kr = KC ? KC : (int)p.conv_k;
 
-    // the role's 256 staged channels: lc < 128 the first range (q for role
-    // 0, k for role 1), the rest the second (k, v); global channel of lc
+    // the staged channels, in order: q, k, v (whole record); q, k (W part);
+    // k, v (U part); the global channel of staged channel lc
     auto chan = [&](int lc) -> uint32_t {
-        if (role_w) return lc < kDk ? kh * kDk + lc : key_width + kh * kDk + (lc - kDk);
-        return lc < kDk ? key_width + kh * kDk + lc : 2 * key_width + h * kHeadDv + (lc - kDk);
+        const uint32_t qch = kh * kDk, kch = key_width + kh * kDk, vch = 2 * key_width + h * kHeadDv;
+        if (u_only) return lc < kDk ? kch + lc : vch + (lc - kDk);
+        return lc < kDk ? qch + lc : lc < 2 * kDk ? kch + (lc - kDk) : vch + (lc - 2 * kDk);
     };
-    // conv work of this thread: channel lc over rows 16 half .. + 15 (the
-    // half is wave-uniform)
-    const int lc = tid & (kPin - 1);
+    // conv work of this thread (row ranges wave-uniform): channel lc of the
+    // first 256 over rows 16 half .. + 15; for the whole record also v channel vch
+    // over rows 8 vquart .. + 7
+    const int lc = tid & (2 * kDk - 1);
     const int half = tid >> 8;
-    const uint32_t ch = chan(lc);
+    const int vch = tid & (kHeadDv - 1);
+    const int vquart = tid >> 7;
+    const uint32_t ch0 = chan(lc);
+    const uint32_t ch1 = chan(2 * kDk + vch);  // used for the whole record only
     const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
     const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
     // weights and the stored history (used by the rows that start the call;
     // the others take the K-1 inputs before them from the staged rows)
-    Conv cv;
-    cv.load(p.history + (hist_slot + ch) * K1, p.conv_w + (size_t)ch * p.conv_k, p.conv_k);
+    Conv cv0, cvv;
+    cv0.load(p.history + (hist_slot + ch0) * K1, p.conv_w + (size_t)ch0 * p.conv_k, p.conv_k);
+    if constexpr (!kSplit) {
+        cvv.load(p.history + (hist_slot + ch1) * K1, p.conv_w + (size_t)ch1 * p.conv_k, p.conv_k);
+    }
 
     // decay and write strength inputs first: wave 1 turns them into g and
     // beta while the raw inputs below are in flight
@@ -879,7 +902,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     };
     // ---- raw inputs: rows r0 - kPre .. r0 + kCk - 1 of the sequence, clamped
     //      into its rows (clamped copies are never used), in 16-byte segments
-    //      of the two channel ranges, every load in flight together
+    //      of the staged channel ranges, every load in flight together
     {
         uint32_t lt = tid;
         pin(lt);
@@ -889,7 +912,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         };
         constexpr int R = kPre + kCk;
         if (!bf16_in) {
-            constexpr int SEG = kPin / 4;
+            constexpr int SEG = kIn / 4;
             constexpr int N = (R * SEG + kPrepThreads - 1) / kPrepThreads;
             f32x4 xs[N];
 #pragma unroll
@@ -904,7 +927,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
                 if (e < R * SEG) *(f32x4 *)&L.xin[e / SEG][4 * (e % SEG)] = xs[n];
             }
         } else {
-            constexpr int SEG = kPin / 8;
+            constexpr int SEG = kIn / 8;
             constexpr int N = (R * SEG + kPrepThreads - 1) / kPrepThreads;
             u32x4 xs[N];
 #pragma unroll
@@ -929,7 +952,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     __syncthreads();
     // ---- causal conv + silu (math.rs:158-187); rows past nv are zero and do
     //      not advance the history
-    if (c > 0 || half == 1) cv.set_hist(&L.xin[kPre + 16 * half - (Kr - 1)][lc], kPin, p.conv_k);
+    const bool last_chunk = c + 1 == nchunks;
+    if (c > 0 || half == 1) cv0.set_hist(&L.xin[kPre + 16 * half - (Kr - 1)][lc], kIn, p.conv_k);
     {
         const int tb = 16 * half;
         float xr[16];
@@ -938,16 +962,16 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         float yr[16];
         if (tb + 16 <= (int)nv) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) yr[i] = fast_silu(cv.pre(xr[i], p.conv_k));
+            for (int i = 0; i < 16; ++i) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
         } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 yr[i] = 0.0f;
-                if ((uint32_t)(tb + i) < nv) yr[i] = fast_silu(cv.pre(xr[i], p.conv_k));
+                if ((uint32_t)(tb + i) < nv) yr[i] = fast_silu(cv0.pre(xr[i], p.conv_k));
             }
         }
-        // role 0: q -> q, k -> k and kc; role 1: k -> k and kc, v -> vc
-        const bool is_k = role_w ? lc >= kDk : lc < kDk;  // wave-uniform
+        // first range q (k for the U part), second range k (v for the U part)
+        const bool is_k = u_only ? lc < kDk : lc >= kDk;  // wave-uniform
         const int d = lc & (kDk - 1);
         if (is_k) {
 #pragma unroll
@@ -956,7 +980,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             for (int i = 0; i < 16; i += 4) {
                 *(f32x4 *)&L.kc[d][tb + i] = f32x4{yr[i], yr[i + 1], yr[i + 2], yr[i + 3]};
             }
-        } else if (role_w) {
+        } else if (!u_only) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) L.qv.q[tb + i][d] = yr[i];
         } else {
@@ -966,12 +990,30 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             }
         }
         // the history after the call: the last K-1 raw inputs, from the last
-        // chunk, by the half that holds the last row; q/k channels by role 0
-        // of the key head's first value head, v channels by role 1
-        if (c + 1 == nchunks && half == (nv > 16 ? 1 : 0) &&
-            (role_w ? h % groups == 0 : lc >= kDk)) {
-            cv.store(p.history + (hist_next + ch) * K1, p.conv_k);
+        // chunk, by the threads that hold the last row; q/k channels only in
+        // the key head's first value head (a U part writes only its v channels)
+        const bool writes = u_only ? lc >= kDk : h % groups == 0;
+        if (last_chunk && half == (nv > 16 ? 1 : 0) && writes) {
+            cv0.store(p.history + (hist_next + ch0) * K1, p.conv_k);
         }
+    }
+    if constexpr (!kSplit) {
+        if (c > 0 || vquart > 0) {
+            cvv.set_hist(&L.xin[kPre + 8 * vquart - (Kr - 1)][2 * kDk + vch], kIn, p.conv_k);
+        }
+        const int tb = 8 * vquart;
+        float xr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xr[i] = L.xin[kPre + tb + i][2 * kDk + vch];
+        float yv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            yv[i] = 0.0f;
+            if ((uint32_t)(tb + i) < nv) yv[i] = fast_silu(cvv.pre(xr[i], p.conv_k));
+        }
+        *(f32x4 *)&L.qv.vc[vch][tb] = f32x4{yv[0], yv[1], yv[2], yv[3]};
+        *(f32x4 *)&L.qv.vc[vch][tb + 4] = f32x4{yv[4], yv[5], yv[6], yv[7]};
+        if (last_chunk && vquart == (int)(nv - 1) / 8) cvv.store(p.history + (hist_next + ch1) * K1, p.conv_k);
     }
     __syncthreads();
     // ---- L2 norms per row (math.rs:218-219): 16 lanes per row, 8 dims each,
@@ -983,25 +1025,26 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 0; i < 2; ++i) {
             const float4 b4 = *(const float4 *)&L.k[t][8 * part + 4 * i];
             sk += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
-            if (role_w) {
+            if (kW) {
                 const float4 a4 = *(const float4 *)&L.qv.q[t][8 * part + 4 * i];
                 sq += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
             }
         }
         sk = sum16(sk);
-        if (role_w) sq = sum16(sq);
+        if (kW) sq = sum16(sq);
         if (part == 0) {
             const float rk = 1.0f / sqrtf(sk + 1e-6f);
             const float gt = L.g[t], bt = L.beta[t];
             L.rk[t] = rk;
-            if (role_w) {
+            if (kW) {
                 // Qe's row scale e^{g_t} / |q_t|; W's column scale of T,
                 // beta_j e^{g_j} / |k_j|
                 const float rq = 1.0f / sqrtf(sq + 1e-6f);
                 L.rq[t] = rq;
                 L.qs[t] = rq * fast_exp(gt);
                 L.sw[t] = bt * fast_exp(gt) * rk;
-            } else {
+            }
+            if (kU) {
                 // U's column scale beta_j; Ks's e^{g_C - g_j} / |k_j|
                 L.su[t] = bt;
                 L.ss[t] = fast_exp(L.g[kCk - 1] - gt) * rk;
@@ -1009,15 +1052,24 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         }
     }
     __syncthreads();
-    // ---- P1: the k.k tiles (0,0), (1,0), (1,1) -> A on waves 0..2.  Role 0
-    //      also the q.k tiles: wave 3 (0,0) -> Pm (and Pm's zero tile (0,1)),
+    // ---- P1: the k.k tiles (0,0), (1,0), (1,1) -> A on waves 0..2.  With W:
+    //      the q.k tiles too, wave 3 (0,0) -> Pm (and Pm's zero tile (0,1)),
     //      waves 4..7 halves over k of (1,0) (waves 4, 6) and (1,1) (5, 7),
     //      the second halves handed over in LDS, so every SIMD runs 48 MFMAs;
-    //      waves 4..7 then write Qe.  Role 1: waves 3..7 write Ks.
+    //      waves 4..7 then write Qe (and with U, Ks).  U alone: waves 3..7
+    //      write Ks.
     f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
     const int p1_tile = wave < 3 ? wave : wave == 3 ? 0 : 1 + (wave & 1);
     const int p1_tr = p1_tile == 0 ? 0 : 1, p1_tc = p1_tile == 2 ? 1 : 0;
-    if (wave < 3 || role_w) {
+    auto write_ks = [&](int first, int stride) __attribute__((always_inline)) {
+        // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
+        for (int e = first; e < kDk * kCk / 4; e += stride) {
+            const int d = e >> 3, j = 4 * (e & 7);
+            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
+                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
+        }
+    };
+    if (wave < 3 || kW) {
         const float *arow = wave < 3 ? &L.k[16 * p1_tr][0] : &L.qv.q[16 * p1_tr][0];
         constexpr int NH = kDk / 32;
         // k range: both halves (waves 0..3), the first (4, 5) or second (6, 7)
@@ -1036,7 +1088,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         }
         acc += acc2;
     }
-    if (wave < 3 || (role_w && wave == 3)) {
+    if (wave < 3 || (kW && wave == 3)) {
         const int j = 16 * p1_tc + r16;
         const float gj = L.g[j], rkj = L.rk[j];
 #pragma unroll
@@ -1050,7 +1102,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
                 rec[kRecPm + t * kCk + 16 + r16] = 0.0f;
             }
         }
-    } else if (role_w) {
+    } else if (kW) {
         if (wave >= 6) L.part[wave & 1][lane] = acc;
         const int u = tid - 4 * 64;  // 0..255
 #pragma unroll
@@ -1060,19 +1112,15 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             const int t = e >> 5, d = 4 * (e & 31);
             *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.qv.q[t][d] * L.qs[t];
         }
+        if (kU) write_ks(u, 256);
     } else {
-        // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
-        for (int e = tid - 3 * 64; e < kDk * kCk / 4; e += kPrepThreads - 3 * 64) {
-            const int d = e >> 3, j = 4 * (e & 7);
-            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
-                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
-        }
+        write_ks(tid - 3 * 64, kPrepThreads - 3 * 64);
     }
     __syncthreads();
     // ---- P2: T = (I + A)^-1.  Waves 0 and 1 invert the diagonal 16 x 16
     //      blocks by forward substitution (lane j: column j), storing T and
-    //      its transpose; wave 2 clears the upper-right block; role 1's wave
-    //      3 writes e^{g_C}; role 0's waves 4 and 5 finish their Pm tiles.
+    //      its transpose; wave 2 clears the upper-right block; wave 3 writes
+    //      e^{g_C} (with U); waves 4 and 5 finish their Pm tiles (with W).
     if (wave < 2) {
         const int b0 = 16 * wave;
         const int j = r16;
@@ -1081,30 +1129,30 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 1; i < 16; ++i)
 #pragma unroll
             for (int qd = 0; 4 * qd < i; ++qd) ar[i][qd] = *(const f32x4 *)&L.a[b0 + i][b0 + 4 * qd];
-        float x[16];
+        float xv[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float acc0 = i == j ? 1.0f : 0.0f, acc1 = 0.0f;
 #pragma unroll
             for (int mm = 0; mm < i; ++mm) {
                 const float am = ar[i][mm >> 2][mm & 3];
-                if (mm & 1) acc1 -= am * x[mm];
-                else acc0 -= am * x[mm];
+                if (mm & 1) acc1 -= am * xv[mm];
+                else acc0 -= am * xv[mm];
             }
-            x[i] = acc0 + acc1;
+            xv[i] = acc0 + acc1;
         }
         if (lane < 16) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                L.t[b0 + i][b0 + j] = x[i];
-                L.tt[b0 + j][b0 + i] = x[i];
+                L.t[b0 + i][b0 + j] = xv[i];
+                L.tt[b0 + j][b0 + i] = xv[i];
             }
         }
     } else if (wave == 2) {
         for (int e = lane; e < 256; e += 64) L.t[e >> 4][16 + (e & 15)] = 0.0f;
     } else if (wave == 3) {
-        if (!role_w && lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
-    } else if (wave < 6 && role_w) {
+        if (kU && lane == 0) rec[kRecEc] = expf(L.g[kCk - 1]);
+    } else if (wave < 6 && kW) {
         acc += L.part[wave & 1][lane];
         const int j = 16 * p1_tc + r16;
         const float gj = L.g[j], rkj = L.rk[j];
@@ -1135,35 +1183,36 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 0; i < 4; ++i) L.t[16 + 4 * sl + i][r16] = -t21[i];
     }
     __syncthreads();
-    // ---- P3: role 0 W = T diag(sw) K (stored negated), role 1
-    //      U = T diag(su) V; wave w owns rows 16 (w & 1).. and columns
+    // ---- P3: W = T diag(sw) K (stored negated) and U = T diag(su) V, those
+    //      of this mode; wave w owns rows 16 (w & 1).. and columns
     //      32 (w >> 1) .. + 31
     {
         const int tr = wave & 1, c0 = 32 * (wave >> 1);
-        Ops<2> ta;
-        load_ops(ta, &L.t[16 * tr][0], kPc, lane);
-        scale_ops(ta, role_w ? L.sw : L.su, lane);
-        Ops<2> xb[2];
+        auto product = [&](const float *scale, const float (*rows)[kPc], float *dst, float sign)
+                           __attribute__((always_inline)) {
+            Ops<2> ta;
+            load_ops(ta, &L.t[16 * tr][0], kPc, lane);
+            scale_ops(ta, scale, lane);
+            Ops<2> xb[2];
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
-            load_ops(xb[n], role_w ? &L.kc[c0 + 16 * n][0] : &L.qv.vc[c0 + 16 * n][0], kPc, lane);
-        }
-        f32x4 o[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+            for (int n = 0; n < 2; ++n) load_ops(xb[n], &rows[c0 + 16 * n][0], kPc, lane);
+            f32x4 o[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+            for (int st = 0; st < 2; ++st)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+                for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int n = 0; n < 2; ++n) o[n] = mfma4(ta.v[st][e], xb[n].v[st][e], o[n]);
-        float *dst = rec + (role_w ? kRecWn : kRecU);
-        const float sign = role_w ? -1.0f : 1.0f;
+                    for (int n = 0; n < 2; ++n) o[n] = mfma4(ta.v[st][e], xb[n].v[st][e], o[n]);
 #pragma unroll
-        for (int n = 0; n < 2; ++n)
+            for (int n = 0; n < 2; ++n)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
-                dst[t * kDk + col] = sign * o[n][i];
-            }
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
+                    dst[t * kDk + col] = sign * o[n][i];
+                }
+        };
+        if (kW) product(L.sw, L.kc, rec + kRecWn, -1.0f);
+        if (kU) product(L.su, L.qv.vc, rec + kRecU, 1.0f);
     }
 }
 
@@ -1340,25 +1389,35 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
     }
 }
 
-template <class Conv>
+template <class Conv, bool kSplit>
 hipError_t launch_chunk_prep(hipStream_t stream, const GdnParams &p, uint32_t max_chunks) {
     static bool configured = false;
     if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_prep_kernel<Conv>,
+        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_prep_kernel<Conv, kSplit>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)sizeof(PrepLds));
+                                                 (int)sizeof(PrepLds<kSplit>));
         if (e != hipSuccess) return e;
         configured = true;
     }
-    SR_LAUNCH("gdn_chunk_prep_kernel", gdn_chunk_prep_kernel<Conv>,
-              dim3(2 * p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads), sizeof(PrepLds), stream,
-              p);
+    SR_LAUNCH("gdn_chunk_prep_kernel", (gdn_chunk_prep_kernel<Conv, kSplit>),
+              dim3((kSplit ? 2 : 1) * p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads),
+              sizeof(PrepLds<kSplit>), stream, p);
     return hipGetLastError();
 }
 
-hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t max_chunks) {
-    const hipError_t e = p.conv_k == 4 ? launch_chunk_prep<ConvK<4>>(stream, p, max_chunks)
-                                       : launch_chunk_prep<ConvChan>(stream, p, max_chunks);
+// records: the launch's (chunk, value head) pairs; the prep takes two
+// workgroups per record when that still fits the CUs
+hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t max_chunks,
+                        uint64_t records, int num_cus) {
+    const bool split = 2 * records <= (uint64_t)(num_cus > 0 ? num_cus : 1);
+    hipError_t e;
+    if (p.conv_k == 4) {
+        e = split ? launch_chunk_prep<ConvK<4>, true>(stream, p, max_chunks)
+                  : launch_chunk_prep<ConvK<4>, false>(stream, p, max_chunks);
+    } else {
+        e = split ? launch_chunk_prep<ConvChan, true>(stream, p, max_chunks)
+                  : launch_chunk_prep<ConvChan, false>(stream, p, max_chunks);
+    }
     if (e != hipSuccess) return e;
     const uint32_t pairs = p.nseq * p.value_heads;
     const uint32_t xcd_map = pairs % 8 == 0 ? 1u : 0u;
@@ -1540,7 +1599,8 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs
                           dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
             }
         } else if (chunk_kernel) {
-            const hipError_t e = launch_chunk(stream, p, max_chunks);
+            const hipError_t e =
+                launch_chunk(stream, p, max_chunks, (uint64_t)chunks * pool->value_heads, g.num_cus);
             if (e != hipSuccess) return e;
         } else {
             const uint32_t blocks = (uint32_t)n * pool->value_heads * (pool->value_dim / kRows);

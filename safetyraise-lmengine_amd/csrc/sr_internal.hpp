@@ -318,6 +318,7 @@ struct GdnLaunch {
     uint32_t rec_stride = 0, keep_rows = 0;
     // chunked prefill: gdn_chunk_rec_bytes(...) bytes of per-chunk records
     float *chunk_rec = nullptr;
+    int num_cus = 256;
 };
 
 // One sequence of a GDN launch: pool slot, its rows in the call, the

@@ -322,3 +322,29 @@ def test_gdn_chunked_form_more_than_64_sequences(pkg, backend, rng):
     rows[3] = 40
     run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, "70 sequences")
     pool.destroy()
+
+
+def test_gdn_chunked_form_long_calls_take_the_one_workgroup_prep(pkg, backend, rng):
+    # a call with more (chunk, value head) records than half the CUs takes
+    # the prep form with one workgroup per record (fewer take two): 5 chunks
+    # x 32 value heads, conv kernel 3 (run-time taps), f32 host inputs, then
+    # bf16 device inputs with a partial last chunk, then a short call
+    import torch
+    L = Layer(rng, 16, 32, 128, 128, 3)
+    pool = pkg.GdnState(backend, 16, 32, 128, 128, 3, 2)
+    s = pool.open()
+    m, h = seeded_state(rng, L)
+    pool.write(s, m, h)
+    run_batch(pkg, backend, pool, L, [s], [160], [(m, h)], rng, "160 rows f32")
+    qkv, z, av, bv = (O.bf16_round(t) for t in L.inputs(rng, 150))
+    exp = oracle_rows(L, (qkv, z, av, bv), m, h)
+    dev = [torch.from_numpy(t).to(torch.bfloat16).cuda() for t in (qkv, z, av, bv)]
+    out = torch.zeros((150, L.hv * L.dv), device="cuda")
+    w = [torch.from_numpy(t).cuda() for t in (L.a_log, L.dt_bias, L.conv, L.norm)]
+    pkg.gdn_forward(backend, pool, [s], [150], *dev, *w, out, eps=1e-6)
+    close(out.cpu().numpy(), exp, what="150 rows bf16")
+    gm, gh = pool.read(s)
+    close(gm, m, what="state after 150 rows")
+    close(gh, h, atol=0, rtol=0, what="history after 150 rows")
+    run_batch(pkg, backend, pool, L, [s], [40], [(m, h)], rng, "40 rows after")
+    pool.destroy()
