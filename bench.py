@@ -738,8 +738,9 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
             "unit": "TFLOP/s", "frac": round(chunk_tf / MFMA_F32_PEAK_TFS, 4),
             "frac_token_serial": round(serial_tf / MFMA_F32_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("gdn_prefill_qwen35"),
-            "kernel": "gdn_chunk_prep_kernel<ConvK<4>> + gdn_chunk_scan_kernel (the call's "
-                      "chunked form: sum of the two kernels' mean durations)",
+            "kernel": "gdn_chunk_prep_kernel<ConvK<4>, true> + gdn_chunk_scan_kernel (the "
+                      "call's chunked form, its prep with two workgroups per record: sum of the "
+                      "two kernels' mean durations)",
             "launch_us_mean": round(float(chunk_us), 2),
             "flops_per_launch": int(chunked_form / nchunk),
             "flops_per_step": int(chunked_form),
