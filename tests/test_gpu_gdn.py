@@ -277,7 +277,8 @@ def test_gdn_device_views_at_odd_offsets(pkg, backend, rng):
     import torch
     L = Layer(rng, 16, 32)
     pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 2)
-    for rows, bf16 in ((40, False), (40, True), (3, False)):
+    for rows, bf16, odd_qkv in ((40, False, False), (40, True, False), (3, False, False),
+                                (40, False, True)):
         s = pool.open()
         m, h = seeded_state(rng, L)
         pool.write(s, m, h)
@@ -293,13 +294,15 @@ def test_gdn_device_views_at_odd_offsets(pkg, backend, rng):
             buf[1:] = flat.cuda()
             return buf[1:].view(t.shape)
 
-        dev = [torch.from_numpy(qkv).to(dt).cuda(), odd(z, dt),
+        # a qkv view one element in is not 16-byte aligned: such a call takes
+        # the row-block kernel instead of the chunked form
+        dev = [odd(qkv, dt) if odd_qkv else torch.from_numpy(qkv).to(dt).cuda(), odd(z, dt),
                torch.from_numpy(av).to(dt).cuda(), torch.from_numpy(bv).to(dt).cuda()]
         w = [torch.from_numpy(t).cuda() for t in (L.a_log, L.dt_bias, L.conv)] + [odd(L.norm, torch.float32)]
         out = odd(np.zeros((rows, L.hv * L.dv), np.float32), torch.float32)
         pkg.gdn_forward(backend, pool, [s], [rows], *dev, *w, out, eps=1e-6)
-        close(out.cpu().numpy(), exp, what=f"rows {rows} bf16 {bf16}")
-        close(pool.read(s)[0], m, what=f"state rows {rows} bf16 {bf16}")
+        close(out.cpu().numpy(), exp, what=f"rows {rows} bf16 {bf16} odd qkv {odd_qkv}")
+        close(pool.read(s)[0], m, what=f"state rows {rows} bf16 {bf16} odd qkv {odd_qkv}")
         pool.close(s)
     pool.destroy()
 
