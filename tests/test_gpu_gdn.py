@@ -351,3 +351,45 @@ def test_gdn_chunked_form_long_calls_take_the_one_workgroup_prep(pkg, backend, r
     close(gh, h, atol=0, rtol=0, what="history after 150 rows")
     run_batch(pkg, backend, pool, L, [s], [40], [(m, h)], rng, "40 rows after")
     pool.destroy()
+
+
+def test_gdn_non_unit_norm_weights(pkg, backend, rng):
+    # non-unit per-head norm weights (the other tests use ones): a
+    # decode-sized call (norm in the head kernel), chunked calls of 128 and
+    # 129 rows, then 3 + 129 rows in one call (chunked form, then the norm
+    # kernel), each against the oracle with the state carried
+    L = Layer(rng, 16, 32)
+    L.norm = (1 + 0.1 * rng.standard_normal(L.dv)).astype(np.float32)
+    pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 2)
+    a, b = pool.open(), pool.open()
+    ra, rb = seeded_state(rng, L), seeded_state(rng, L)
+    pool.write(a, *ra)
+    pool.write(b, *rb)
+    for call, (seqs, rows, refs) in enumerate((([a], [5], [ra]), ([a], [128], [ra]),
+                                               ([a], [129], [ra]), ([a, b], [3, 129], [ra, rb]))):
+        run_batch(pkg, backend, pool, L, seqs, rows, refs, rng, f"call {call} rows {rows}")
+    pool.destroy()
+
+
+def test_gdn_non_finite_output_is_reported(pkg, backend, rng):
+    # an infinite value input makes the row's delta-rule output non-finite,
+    # which the per-head RMSNorm rejects (math.rs:39-41): a decode-sized call
+    # (norm in the head kernel) and chunked calls of 64 and 160 rows (norm
+    # kernel); the error word is cleared by the report, so a clean call
+    # afterwards succeeds
+    L = Layer(rng, 2, 4)
+    pool = pkg.GdnState(backend, 2, 4, 128, 128, 4, 4)
+    for rows in (3, 64, 160):
+        s = pool.open()
+        x = L.inputs(rng, rows)
+        x[0][rows // 2, 2 * L.hk * L.dk + 5] = np.inf  # a value channel of head 0
+        with pytest.raises(pkg.PluginError, match="variance"):
+            plugin_rows(pkg, backend, pool, L, [s], [rows], x)
+        pool.close(s)
+    s = pool.open()
+    m = np.zeros((L.hv, L.dv, L.dk), np.float32)
+    h = np.zeros((L.C, L.K - 1), np.float32)
+    x = L.inputs(rng, 64)
+    close(plugin_rows(pkg, backend, pool, L, [s], [64], x), oracle_rows(L, x, m, h),
+          what="clean call after the errors")
+    pool.destroy()
