@@ -664,7 +664,10 @@ __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(1.4426950408889634f * x);
 }
 
-// One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.
+// One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.  Qe,
+// -W, Ks and Pm are the scan's MFMA operands and are stored as their two
+// bf16 parts (the hi plane, then the lo plane, in the matrix's own floats);
+// U and e^{g_C} stay f32.
 constexpr int kRecQe = 0;                      // [kCk][kDk]     Qe
 constexpr int kRecWn = kRecQe + kCk * kDk;     // [kCk][kDk]     -W
 constexpr int kRecU = kRecWn + kCk * kDk;      // [kCk][kHeadDv] U
@@ -674,17 +677,53 @@ constexpr int kRecEc = kRecPm + kCk * kCk;     // e^{g_C}
 constexpr int kRecFloats = kRecEc + 64;        // a 256-byte multiple
 constexpr int kPre = kMaxK - 1;                // raw input rows staged before a chunk
 
+// The scan's products run on bf16 MFMA with each f32 operand split in two
+// parts, hi = bf16(x) and lo = bf16(x - hi) (round to nearest even; x - hi
+// is exact), and a product taken as hi.hi + hi.lo + lo.hi: every part
+// product is exact in f32, and what is left out (lo.lo and the remainder
+// x - hi - lo) is below 2^-15 of the product.  A matrix lives in LDS as its
+// two part planes, rows padded against bank conflicts.
+constexpr int kPh = kDk + 8;  // pitch (bf16) of [.][Dk] planes
+constexpr int kPq = kCk + 8;  // pitch (bf16) of [.][chunk] planes
+
+template <int R, int P>
+struct Parts {
+    uint16_t hi[R][P];
+    uint16_t lo[R][P];
+};
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Element i (or four from i) of an n-element record matrix at float offset
+// `off`, written as its parts: hi plane at element i, lo plane at n + i.
+__device__ __forceinline__ void rec_put1(float *rec, int off, int n, int i, float x) {
+    uint16_t *m = (uint16_t *)(rec + off);
+    const __bf16 hi = (__bf16)x;
+    const __bf16 lo = (__bf16)(x - (float)hi);
+    m[i] = __builtin_bit_cast(uint16_t, hi);
+    m[n + i] = __builtin_bit_cast(uint16_t, lo);
+}
+__device__ __forceinline__ void rec_put4(float *rec, int off, int n, int i, const f32x4 &x) {
+    uint16_t *m = (uint16_t *)(rec + off);
+    const bf16x4 hi = __builtin_convertvector(x, bf16x4);
+    const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
+    *(bf16x4 *)(m + i) = hi;
+    *(bf16x4 *)(m + n + i) = lo;
+}
+
 struct ScanLds {
-    float s0[kVs][kPr];  // state slice: rows v, dims d
-    float dt[kVs][kPc];  // Delta of the slice, transposed: [v][t]
-    struct Rec {         // a chunk's record, rows padded against bank conflicts
-        float qe[kCk][kPr];
-        float wn[kCk][kPr];
-        float ks[kDk][kPc];
-        float pm[kCk][kPc];
-        float u[kCk][kPc];  // this slice's columns of U
+    Parts<kVs, kPh> s0;  // state slice parts: rows v, dims d
+    Parts<kVs, kPq> dt;  // Delta of the slice, transposed: [v][t]
+    struct Rec {         // a chunk's record
+        Parts<kCk, kPh> qe;
+        Parts<kCk, kPh> wn;
+        Parts<kDk, kPq> ks;
+        Parts<kCk, kPq> pm;
+        float u[kCk][kPc];  // this slice's columns of U, f32 (the Delta accumulators' start)
     } r[2];
 };
+static_assert(sizeof(ScanLds) <= 160 * 1024, "scan LDS");
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -727,6 +766,52 @@ __device__ __forceinline__ void mma(f32x4 &acc, const Ops<NK> &a, const Ops<NK> 
         acc = mfma4(a.v[s].z, b.v[s].z, acc);
         acc = mfma4(a.v[s].w, b.v[s].w, acc);
     }
+}
+
+// Four consecutive elements of row `row` from column `col` into the planes.
+template <int R, int P>
+__device__ __forceinline__ void put_parts(Parts<R, P> &m, int row, int col, const f32x4 &x) {
+    const bf16x4 hi = __builtin_convertvector(x, bf16x4);
+    const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
+    *(bf16x4 *)&m.hi[row][col] = hi;
+    *(bf16x4 *)&m.lo[row][col] = lo;
+}
+
+// One lane's parts of a 16-row tile over NS steps of 32 k: row lane & 15,
+// k = 32 s + 8 (lane >> 4) + j, the v_mfma_f32_16x16x32_bf16 operand layout
+// (A row r and B row r at the same k; the tile's rows 4 slot + i, column r
+// are acc[i], as for the f32 form).
+template <int NS>
+struct Ops2 {
+    bf16x8 hi[NS], lo[NS];
+};
+
+template <int NS, int R, int P>
+__device__ __forceinline__ void load_ops2(Ops2<NS> &o, const Parts<R, P> &m, int row0, int lane) {
+    const int r = row0 + (lane & 15), c = 8 * (lane >> 4);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        o.hi[s] = *(const bf16x8 *)&m.hi[r][32 * s + c];
+        o.lo[s] = *(const bf16x8 *)&m.lo[r][32 * s + c];
+    }
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc + A B^T: the hi.hi products accumulate onto acc, the two cross terms in
+// a second chain that is added at the end.
+template <int NS>
+__device__ __forceinline__ f32x4 mma2(f32x4 acc, const Ops2<NS> &a, const Ops2<NS> &b) {
+    f32x4 x = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        acc = mfma_bf16(a.hi[s], b.hi[s], acc);
+        x = mfma_bf16(a.hi[s], b.lo[s], x);
+        x = mfma_bf16(a.lo[s], b.hi[s], x);
+    }
+    return acc + x;
 }
 
 // Causal conv channel with the kernel size K known at compile time; same
@@ -1065,8 +1150,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
         for (int e = first; e < kDk * kCk / 4; e += stride) {
             const int d = e >> 3, j = 4 * (e & 7);
-            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
-                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
+            rec_put4(rec, kRecKs, kDk * kCk, d * kCk + j,
+                     *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j]);
         }
     };
     if (wave < 3 || kW) {
@@ -1098,8 +1183,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             if (wave < 3) {
                 L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * acc[i] : 0.0f;
             } else {
-                rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
-                rec[kRecPm + t * kCk + 16 + r16] = 0.0f;
+                rec_put1(rec, kRecPm, kCk * kCk, t * kCk + j, e * L.rq[t] * rkj * acc[i]);
+                rec_put1(rec, kRecPm, kCk * kCk, t * kCk + 16 + r16, 0.0f);
             }
         }
     } else if (kW) {
@@ -1110,7 +1195,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             // Qe = diag(e^{g_t} / |q_t|) Q
             const int e = u + n * 256;
             const int t = e >> 5, d = 4 * (e & 31);
-            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.qv.q[t][d] * L.qs[t];
+            rec_put4(rec, kRecQe, kCk * kDk, t * kDk + d, *(const f32x4 *)&L.qv.q[t][d] * L.qs[t]);
         }
         if (kU) write_ks(u, 256);
     } else {
@@ -1160,7 +1245,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * p1_tr + 4 * sl + i;
             const float e = j <= t ? fast_exp(L.g[t] - gj) : 0.0f;
-            rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
+            rec_put1(rec, kRecPm, kCk * kCk, t * kCk + j, e * L.rq[t] * rkj * acc[i]);
         }
     }
     __syncthreads();
@@ -1188,7 +1273,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     //      32 (w >> 1) .. + 31
     {
         const int tr = wave & 1, c0 = 32 * (wave >> 1);
-        auto product = [&](const float *scale, const float (*rows)[kPc], float *dst, float sign)
+        // -W goes to the record as its parts, U as f32
+        auto product = [&](const float *scale, const float (*rows)[kPc], int off, bool parts)
                            __attribute__((always_inline)) {
             Ops<2> ta;
             load_ops(ta, &L.t[16 * tr][0], kPc, lane);
@@ -1208,11 +1294,12 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
-                    dst[t * kDk + col] = sign * o[n][i];
+                    if (parts) rec_put1(rec, off, kCk * kDk, t * kDk + col, -o[n][i]);
+                    else rec[off + t * kDk + col] = o[n][i];
                 }
         };
-        if (kW) product(L.sw, L.kc, rec + kRecWn, -1.0f);
-        if (kU) product(L.su, L.qv.vc, rec + kRecU, 1.0f);
+        if (kW) product(L.sw, L.kc, kRecWn, true);
+        if (kU) product(L.su, L.qv.vc, kRecU, false);
     }
 }
 
@@ -1256,48 +1343,53 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
     const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
 
-    // record staging: 7 16-byte segments per thread; segment e = tid + 512 n
-    // is in Qe (n < 2), -W (n < 4), Ks (n < 6), then Pm (waves 0..3) or U
+    // record staging: 7 16-byte segments per thread.  Qe, -W and Ks are
+    // 1024 segments each in the record, hi plane then lo plane: segment
+    // e = tid + 512 (n & 1) is in plane n & 1.  The last segment is Pm's
+    // (output waves: 256 segments, plane t2 >> 7) or this slice's U columns.
     constexpr int kSeg = 7;
     auto rec_of = [&](uint32_t c) -> const float * {
         return p.chunk_rec + ((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats;
     };
     const int t2 = tid & 255;
-    auto fetch = [&](const float *rec, f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+    auto fetch = [&](const float *rec, u32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
 #pragma unroll
         for (int n = 0; n < kSeg; ++n) {
             const int e = tid + kScanThreads * (n & 1);
             int src;
-            if (n < 2) src = kRecQe + (e >> 5) * kDk + 4 * (e & 31);
-            else if (n < 4) src = kRecWn + (e >> 5) * kDk + 4 * (e & 31);
-            else if (n < 6) src = kRecKs + (e >> 3) * kCk + 4 * (e & 7);
-            else if (out_wave) src = kRecPm + (t2 >> 3) * kCk + 4 * (t2 & 7);
+            if (n < 2) src = kRecQe + 4 * e;
+            else if (n < 4) src = kRecWn + 4 * e;
+            else if (n < 6) src = kRecKs + 4 * e;
+            else if (out_wave) src = kRecPm + 4 * t2;
             else src = kRecU + (t2 >> 3) * kHeadDv + vq * kVs + 4 * (t2 & 7);
-            xs[n] = *(const f32x4 *)(rec + src);
+            xs[n] = *(const u32x4 *)(rec + src);
         }
     };
-    auto put = [&](ScanLds::Rec &r, const f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+    auto put = [&](ScanLds::Rec &r, const u32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
 #pragma unroll
         for (int n = 0; n < kSeg; ++n) {
-            const int e = tid + kScanThreads * (n & 1);
-            float *dst;
-            if (n < 2) dst = &r.qe[e >> 5][4 * (e & 31)];
-            else if (n < 4) dst = &r.wn[e >> 5][4 * (e & 31)];
-            else if (n < 6) dst = &r.ks[e >> 3][4 * (e & 7)];
-            else if (out_wave) dst = &r.pm[t2 >> 3][4 * (t2 & 7)];
-            else dst = &r.u[t2 >> 3][4 * (t2 & 7)];
-            *(f32x4 *)dst = xs[n];
+            uint16_t *dst;
+            if (n < 2) dst = (n & 1 ? r.qe.lo : r.qe.hi)[tid >> 4] + 8 * (tid & 15);
+            else if (n < 4) dst = (n & 1 ? r.wn.lo : r.wn.hi)[tid >> 4] + 8 * (tid & 15);
+            else if (n < 6) dst = (n & 1 ? r.ks.lo : r.ks.hi)[tid >> 2] + 8 * (tid & 3);
+            else if (out_wave) dst = (t2 >> 7 ? r.pm.lo : r.pm.hi)[(t2 & 127) >> 2] + 8 * (t2 & 3);
+            else dst = (uint16_t *)&r.u[t2 >> 3][4 * (t2 & 7)];
+            *(u32x4 *)dst = xs[n];
         }
     };
-    f32x4 xs[kSeg];
+    u32x4 xs[kSeg];
     fetch(rec_of(0), xs);
     float *state = p.state + (((size_t)m.state_in * p.value_heads + h) * kHeadDv + vq * kVs) * kDk;
-    {
-        const int v = tid >> 4, d0 = (tid & 15) * 4;
+    // The Delta waves own the slice's f32 state in registers: wave (tr, tc)
+    // state rows 16 tr + (lane & 15), dims 64 tc + 16 n + 4 (lane >> 4) + i,
+    // the layout of their state-update tiles; LDS holds its parts
+    const int sv = 16 * tr + r16;
+    f32x4 s0r[4];
+    if (!out_wave) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *(float4 *)&L.s0[v][d0 + 64 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 64 * i);
-        }
+        for (int n = 0; n < 4; ++n) s0r[n] = *(const f32x4 *)(state + (size_t)sv * kDk + 64 * tc + 16 * n + 4 * sl);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) put_parts(L.s0, sv, 64 * tc + 16 * n + 4 * sl, s0r[n]);
     }
     put(L.r[0], xs);
     if (nchunks > 1) fetch(rec_of(1), xs);
@@ -1308,33 +1400,24 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
         ScanLds::Rec &R = L.r[c & 1];
         // phase 1, tile (rows 16 tr.., state rows 16 tc..): output waves
         // Qe S0^T, Delta waves U + (-W) S0^T
-        Ops<kDk / 16> xa, sb;
-        load_ops(xa, out_wave ? &R.qe[16 * tr][0] : &R.wn[16 * tr][0], kPr, lane);
-        load_ops(sb, &L.s0[16 * tc][0], kPr, lane);
-        f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
+        Ops2<kDk / 32> xa, sb;
+        load_ops2(xa, out_wave ? R.qe : R.wn, 16 * tr, lane);
+        load_ops2(sb, L.s0, 16 * tc, lane);
+        f32x4 acc = {0, 0, 0, 0};
         if (!out_wave) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = R.u[16 * tr + 4 * sl + i][16 * tc + r16];
         }
-#pragma unroll
-        for (int st = 0; st < kDk / 16; ++st)
-#pragma unroll
-            for (int e = 0; e < 4; e += 2) {
-                acc = mfma4(xa.v[st][e], sb.v[st][e], acc);
-                acc2 = mfma4(xa.v[st][e + 1], sb.v[st][e + 1], acc2);
-            }
-        acc += acc2;
-        if (!out_wave) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) L.dt[16 * tc + r16][16 * tr + 4 * sl + i] = acc[i];
-        }
+        acc = mma2(acc, xa, sb);
+        // Delta^T: [v = 16 tc + r16][t = 16 tr + 4 sl + i]
+        if (!out_wave) put_parts(L.dt, 16 * tc + r16, 16 * tr + 4 * sl, acc);
         __syncthreads();
         if (out_wave) {
             // o += Pm Delta
-            Ops<2> pa, db;
-            load_ops(pa, &R.pm[16 * tr][0], kPc, lane);
-            load_ops(db, &L.dt[16 * tc][0], kPc, lane);
-            mma(acc, pa, db);
+            Ops2<1> pa, db;
+            load_ops2(pa, R.pm, 16 * tr, lane);
+            load_ops2(db, L.dt, 16 * tc, lane);
+            acc = mma2(acc, pa, db);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t t = 16 * tr + 4 * sl + i;
@@ -1344,33 +1427,24 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
                 }
             }
         } else {
-            // S_C = e^{g_C} S0 + Delta^T Ks^T over state rows 16 tr.., dims 64 tc..
+            // S_C = e^{g_C} S0 + Delta^T Ks^T over state rows 16 tr.., dims
+            // 64 tc..: tile n is Ks Delta (rows: dims 64 tc + 16 n.., columns:
+            // state rows 16 tr..), the transposed layout of s0r
             const float eC = p.chunk_rec[((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats + kRecEc];
-            Ops<2> da;
-            load_ops(da, &L.dt[16 * tr][0], kPc, lane);
-            Ops<2> kb4[4];
+            Ops2<1> da;
+            load_ops2(da, L.dt, 16 * tr, lane);
+            Ops2<1> kb4[4];
 #pragma unroll
-            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &R.ks[64 * tc + 16 * n][0], kPc, lane);
-            float s0v[4][4];
+            for (int n = 0; n < 4; ++n) load_ops2(kb4[n], R.ks, 64 * tc + 16 * n, lane);
 #pragma unroll
-            for (int n = 0; n < 4; ++n)
+            for (int n = 0; n < 4; ++n) {
+                const f32x4 d = mma2(f32x4{0, 0, 0, 0}, kb4[n], da);
+                s0r[n] = d + eC * s0r[n];
+            }
+            // each of these waves rewrites exactly the S0 parts of its own
+            // rows and dims; all reads of S0 ended before the barrier above
 #pragma unroll
-                for (int i = 0; i < 4; ++i) s0v[n][i] = L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16];
-            f32x4 s4[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-#pragma unroll
-            for (int st = 0; st < 2; ++st)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int n = 0; n < 4; ++n) s4[n] = mfma4(da.v[st][e], kb4[n].v[st][e], s4[n]);
-            // each of these waves rewrites exactly the S0 elements it read
-            // into s0v; all other reads of S0 ended before the barrier above
-#pragma unroll
-            for (int n = 0; n < 4; ++n)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = s4[n][i] + eC * s0v[n][i];
-                }
+            for (int n = 0; n < 4; ++n) put_parts(L.s0, sv, 64 * tc + 16 * n + 4 * sl, s0r[n]);
         }
         // the next chunk's record into the other buffer (last read in the
         // previous chunk), and the loads for the one after
@@ -1380,12 +1454,9 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
         }
         __syncthreads();  // the next chunk reads S0, its record, and rewrites dt
     }
-    {
-        const int v = tid >> 4, d0 = (tid & 15) * 4;
+    if (!out_wave) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            *(float4 *)(state + (size_t)v * kDk + d0 + 64 * i) = *(const float4 *)&L.s0[v][d0 + 64 * i];
-        }
+        for (int n = 0; n < 4; ++n) *(f32x4 *)(state + (size_t)sv * kDk + 64 * tc + 16 * n + 4 * sl) = s0r[n];
     }
 }
 

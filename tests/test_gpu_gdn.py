@@ -393,3 +393,26 @@ def test_gdn_non_finite_output_is_reported(pkg, backend, rng):
     close(plugin_rows(pkg, backend, pool, L, [s], [64], x), oracle_rows(L, x, m, h),
           what="clean call after the errors")
     pool.destroy()
+
+
+def test_gdn_chunked_form_long_recurrence(pkg, backend, rng):
+    # BASELINE config 4's prefill shape on one sequence: 2048 rows in 32
+    # calls of 64 rows, each call and the final state against the oracle
+    # with the state carried.  Once with the config's decays and once with
+    # slow ones (A_log -4: alpha about 0.99 per row), so the state keeps a
+    # long memory of the rounding of the chunked form's products
+    for a_log in (0.0, -4.0):
+        L = Layer(rng, 16, 32)
+        L.a_log = np.full(L.hv, a_log, np.float32)
+        pool = pkg.GdnState(backend, 16, 32, 128, 128, 4, 1)
+        s = pool.open()
+        m = np.zeros((L.hv, L.dv, L.dk), np.float32)
+        h = np.zeros((L.C, L.K - 1), np.float32)
+        for call in range(32):
+            x = L.inputs(rng, 64)
+            close(plugin_rows(pkg, backend, pool, L, [s], [64], x), oracle_rows(L, x, m, h),
+                  what=f"A_log {a_log} call {call}")
+        gm, gh = pool.read(s)
+        close(gm, m, what=f"A_log {a_log} state after 2048 rows")
+        close(gh, h, atol=0, rtol=0, what=f"A_log {a_log} history after 2048 rows")
+        pool.destroy()
