@@ -596,8 +596,10 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 }
 
 // ---------------------------------------------------------------------------
-// Chunked prefill: the delta rule of prefill-sized calls in chunked form on
-// f32 MFMA (v_mfma_f32_16x16x4f32).  With k^, q^ the L2-normalised conv
+// Chunked prefill: the delta rule of prefill-sized calls in chunked form,
+// the chunk-wide products on f32 MFMA (v_mfma_f32_16x16x4f32) and the state
+// products on split bf16 operands (v_mfma_f32_16x16x32_bf16, see Parts
+// below).  With k^, q^ the L2-normalised conv
 // outputs, g_t = sum_{i<=t} log(alpha_i) over the chunk and S0 the state at
 // the chunk start, the token-serial recurrence (math.rs:222-236)
 //     S_t = alpha_t S_{t-1} + delta_t k^_t^T,
