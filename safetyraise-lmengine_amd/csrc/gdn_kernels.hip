@@ -623,7 +623,8 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 //       Pm[t][j] = e^{g_t-g_j} (q^_t . k^_j) (j <= t),  e^{g_C}
 //     and, from the last chunk, the next conv history;
 //   gdn_chunk_scan_kernel: one workgroup per (sequence, value head, 32 of the
-//     Dv = 128 state rows), the slice in LDS, walking the chunks in order:
+//     Dv = 128 state rows), the f32 slice in the registers of the waves that
+//     update it and its bf16 parts in LDS, walking the chunks in order:
 //       Delta = U + (-W) S0^T,  o = (Qe S0^T + Pm Delta) / sqrt(Dk),
 //       S_C = e^{g_C} S0 + Delta^T Ks^T.
 // The conv history is double-buffered exactly as in gdn_delta_kernel.
@@ -1309,9 +1310,10 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
 // state, 8 waves: waves 0..3 own the output tiles (rows 16 (w >> 1)..,
 // state rows 16 (w & 1)..), waves 4..7 the Delta tiles of the same places
 // and then the state-update tiles (state rows 16 ((w - 4) >> 1)..,
-// dims 64 ((w - 4) & 1)..), so each SIMD runs one wave of each kind and the
-// same MFMA count in both phases.  Each chunk's record (Qe, -W, Pm, Ks and
-// this slice's U columns) is staged once per workgroup into LDS,
+// dims 64 ((w - 4) & 1)..), so each SIMD runs one wave of each kind; the
+// latter hold the slice's f32 state in registers between chunks.  Each
+// chunk's record (the parts of Qe, -W, Pm and Ks, and this slice's f32 U
+// columns) is copied once per workgroup into LDS,
 // double-buffered: the loads for chunk c + 1 are issued into registers at
 // the start of chunk c and written to the other buffer at its end, so they
 // have a whole chunk to land.  xcd_map: the grid is ordered so that the four
