@@ -85,7 +85,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_synchronize(
  * every later kernel launch of this context record its device start and end
  * (the timestamps of the dispatch packet, as a profiler's kernel trace sees
  * them); enable == 0 stops and frees the records.  Recording costs one event
- * pair per launch, so timed calls are not the fastest. */
+ * pair per launch, so timed calls are not the fastest.  A window (from one
+ * enable to the next) records at most 65536 launches; later launches run
+ * untimed, so a long run calls enable again to start a new window. */
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_timing_enable(
     safetyraise_kernel_context *context, uint32_t enable);
 /* Waits for the context stream, then reports the index-th distinct kernel
@@ -215,15 +217,24 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
     safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args);
 
 /* safetyraise_kernel_attention_forward that allocates no device memory.  No
- * counterpart in the reference: it is for callers that cannot allocate (code
- * under HIP graph capture, tight serving loops, harnesses that forbid it).
- * Same arguments, kernels and results; DEVICE_POINTERS is required.  The
- * call's scratch (split-K partial records, the per-row RoPE table) comes from
- * a fixed 64 MiB region per GPU that the library holds from the first call on
- * that GPU until the process ends.  A call that needs more fails with
+ * counterpart in the reference: it is for callers that cannot allocate
+ * (tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results; DEVICE_POINTERS is required.  The call's scratch
+ * (split-K partial records, the per-row RoPE table) comes from a fixed
+ * 64 MiB device region per GPU.  The region is a static device array of the
+ * library's code object, so every process that loads the library reserves
+ * it on a GPU when the library's code is first loaded there (its first
+ * kernel launch on that GPU), whether or not it calls this entry point, and
+ * holds it until the process ends.  A call that needs more fails with
  * OUT_OF_MEMORY and its sequences keep their lengths.  Every call on one GPU
  * shares that region, so calls that overlap on one GPU (other threads,
- * contexts or streams) race; calls on one context are serial anyway. */
+ * contexts or streams) race; calls on one context are serial anyway.
+ *
+ * Neither attention entry point can be captured into a HIP graph: a call
+ * appends at the sequences' current lengths and advances those lengths and
+ * the page lists on the host when it is made, so a replay would rewrite the
+ * same cache positions and never advance them.  Both return INVALID_ARGUMENT
+ * while the context's stream is capturing. */
 SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward_noalloc(
     safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args);
 

@@ -415,6 +415,8 @@ using namespace sr;
 extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward(
     safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args) {
     if (context == nullptr) return kInvalid;
+    const int32_t capture = refuse_under_capture(context, "attention_forward");
+    if (capture != kOk) return capture;
     TimerScope timer_scope(context);
     const AttnScratch scratch{grow_partials, grow_rope, context};
     return attention_forward_impl(context, args, scratch);

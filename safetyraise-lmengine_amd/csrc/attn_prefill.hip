@@ -1456,27 +1456,22 @@ uint32_t rows_per_block_dg() {
 
 template <int D, int G, bool kTilePage>
 hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t blocks) {
-    static bool configured = false;
+    // the LDS limits are raised once per instantiation (thread-safe static
+    // initialisers): both kernels take more than the default
     if constexpr (kUsePingPong<D, G>) {
         const size_t lds = kPingPongLds<D> + kRopeStageBytes<D, G>;
-        if (!configured) {
-            const hipError_t e =
-                hipFuncSetAttribute((const void *)attn_prefill_pp_kernel<D, G, kTilePage>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-            configured = true;
-        }
+        static const hipError_t configured =
+            hipFuncSetAttribute((const void *)attn_prefill_pp_kernel<D, G, kTilePage>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (configured != hipSuccess) return configured;
         SR_LAUNCH("attn_prefill_pp_kernel", (attn_prefill_pp_kernel<D, G, kTilePage>), dim3(blocks),
                   dim3(512), lds, stream, p);
     } else {
         const size_t lds = 4 * kTileBytes<D>;  // K and V^T, double buffered
-        if (!configured) {
-            const hipError_t e =
-                hipFuncSetAttribute((const void *)attn_prefill_kernel<D, G, kTilePage>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return e;
-            configured = true;
-        }
+        static const hipError_t configured =
+            hipFuncSetAttribute((const void *)attn_prefill_kernel<D, G, kTilePage>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (configured != hipSuccess) return configured;
         SR_LAUNCH("attn_prefill_kernel", (attn_prefill_kernel<D, G, kTilePage>), dim3(blocks),
                   dim3(64 * G * kLockstepRows<G>), lds, stream, p);
     }
@@ -1935,15 +1930,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_verify_combine_kernel
 template <int D>
 hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
                            uint32_t combine_rows) {
-    static bool configured = false;
     const size_t lds = 8 * kTileBytes<D> + kVerifyPageSlots * sizeof(int32_t);
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)attn_verify_kernel<D>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    static const hipError_t configured = hipFuncSetAttribute(
+        (const void *)attn_verify_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (configured != hipSuccess) return configured;
     SR_LAUNCH("attn_verify_kernel", attn_verify_kernel<D>, dim3(blocks), dim3(kVerifyThreads), lds,
               stream, vp);
     hipError_t e = hipGetLastError();

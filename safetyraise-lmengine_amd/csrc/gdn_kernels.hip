@@ -698,18 +698,31 @@ struct Parts {
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// bf16's largest finite value (0x7F7F).  The hi part of a split is taken
+// from x clamped to it, so a finite x above it still splits into finite
+// parts (x - hi exact); an infinite x leaves a NaN part, and the row's output
+// is non-finite as the reference's would be.
+constexpr float kBf16Max = 3.38953139e38f;
+
+__device__ __forceinline__ float bf16_range(float x) {
+    return __builtin_amdgcn_fmed3f(x, -kBf16Max, kBf16Max);
+}
+__device__ __forceinline__ f32x4 bf16_range(const f32x4 &x) {
+    return f32x4{bf16_range(x.x), bf16_range(x.y), bf16_range(x.z), bf16_range(x.w)};
+}
+
 // Element i (or four from i) of an n-element record matrix at float offset
 // `off`, written as its parts: hi plane at element i, lo plane at n + i.
 __device__ __forceinline__ void rec_put1(float *rec, int off, int n, int i, float x) {
     uint16_t *m = (uint16_t *)(rec + off);
-    const __bf16 hi = (__bf16)x;
+    const __bf16 hi = (__bf16)bf16_range(x);
     const __bf16 lo = (__bf16)(x - (float)hi);
     m[i] = __builtin_bit_cast(uint16_t, hi);
     m[n + i] = __builtin_bit_cast(uint16_t, lo);
 }
 __device__ __forceinline__ void rec_put4(float *rec, int off, int n, int i, const f32x4 &x) {
     uint16_t *m = (uint16_t *)(rec + off);
-    const bf16x4 hi = __builtin_convertvector(x, bf16x4);
+    const bf16x4 hi = __builtin_convertvector(bf16_range(x), bf16x4);
     const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
     *(bf16x4 *)(m + i) = hi;
     *(bf16x4 *)(m + n + i) = lo;
@@ -774,7 +787,7 @@ __device__ __forceinline__ void mma(f32x4 &acc, const Ops<NK> &a, const Ops<NK> 
 // Four consecutive elements of row `row` from column `col` into the planes.
 template <int R, int P>
 __device__ __forceinline__ void put_parts(Parts<R, P> &m, int row, int col, const f32x4 &x) {
-    const bf16x4 hi = __builtin_convertvector(x, bf16x4);
+    const bf16x4 hi = __builtin_convertvector(bf16_range(x), bf16x4);
     const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
     *(bf16x4 *)&m.hi[row][col] = hi;
     *(bf16x4 *)&m.lo[row][col] = lo;
@@ -1466,14 +1479,12 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
 
 template <class Conv, bool kSplit>
 hipError_t launch_chunk_prep(hipStream_t stream, const GdnParams &p, uint32_t max_chunks) {
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t e = hipFuncSetAttribute((const void *)gdn_chunk_prep_kernel<Conv, kSplit>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)sizeof(PrepLds<kSplit>));
-        if (e != hipSuccess) return e;
-        configured = true;
-    }
+    // once per instantiation (a thread-safe static initialiser): its LDS is
+    // above the default limit
+    static const hipError_t configured = hipFuncSetAttribute(
+        (const void *)gdn_chunk_prep_kernel<Conv, kSplit>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(PrepLds<kSplit>));
+    if (configured != hipSuccess) return configured;
     SR_LAUNCH("gdn_chunk_prep_kernel", (gdn_chunk_prep_kernel<Conv, kSplit>),
               dim3((kSplit ? 2 : 1) * p.value_heads, max_chunks, p.nseq), dim3(kPrepThreads),
               sizeof(PrepLds<kSplit>), stream, p);
@@ -1496,14 +1507,10 @@ hipError_t launch_chunk(hipStream_t stream, const GdnParams &p, uint32_t max_chu
     if (e != hipSuccess) return e;
     const uint32_t pairs = p.nseq * p.value_heads;
     const uint32_t xcd_map = pairs % 8 == 0 ? 1u : 0u;
-    static bool configured = false;
-    if (!configured) {
-        const hipError_t e2 = hipFuncSetAttribute((const void *)gdn_chunk_scan_kernel,
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                  (int)sizeof(ScanLds));
-        if (e2 != hipSuccess) return e2;
-        configured = true;
-    }
+    static const hipError_t configured = hipFuncSetAttribute(
+        (const void *)gdn_chunk_scan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)sizeof(ScanLds));
+    if (configured != hipSuccess) return configured;
     SR_LAUNCH("gdn_chunk_scan_kernel", gdn_chunk_scan_kernel, dim3(pairs * (kHeadDv / kVs)),
               dim3(kScanThreads), sizeof(ScanLds), stream, p, xcd_map);
     return hipGetLastError();

@@ -112,13 +112,23 @@ __device__ __forceinline__ f32x8 load8(const void *base, size_t row, uint32_t k,
     return v;
 }
 
+// bf16's largest finite value, 0x7F7F
+constexpr float kBf16Max = 3.38953139e38f;
+
 // x as hi + mid + lo in bf16, each the round-to-nearest-even of what the
-// parts before it leave: exact for |x| in [2^-110, bf16's largest finite
-// value] (below, bits under 2^-133 are lost; above, hi is infinite).  With
-// a bf16 weight the three products are then exact f32 products and their
-// sum is w x up to f32 rounding.
+// parts before it leave: exact for every finite x with |x| >= 2^-110 (below,
+// bits under 2^-133 are lost).  hi is taken from x clamped to bf16's finite
+// range (one v_med3_f32), so a finite x above bf16's largest value still
+// splits exactly (x - hi is then exact and below 2^121).  With a bf16 weight
+// the three products are exact f32 products and their sum is w x up to f32
+// rounding.  An infinite x gives a NaN part, so a product with a non-finite
+// input is non-finite as the reference's is (the ABI call rejects such
+// inputs before any kernel runs, as native/cpu/safetyraise_cpu.c:221-226 does).
 __device__ __forceinline__ void split3(const f32x8 &x, bf16x8 &hi, bf16x8 &mid, bf16x8 &lo) {
-    hi = __builtin_convertvector(x, bf16x8);
+    f32x8 xc;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xc[j] = __builtin_amdgcn_fmed3f(x[j], -kBf16Max, kBf16Max);
+    hi = __builtin_convertvector(xc, bf16x8);
     const f32x8 r1 = x - __builtin_convertvector(hi, f32x8);
     mid = __builtin_convertvector(r1, bf16x8);
     const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);

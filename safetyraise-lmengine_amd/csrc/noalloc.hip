@@ -1,12 +1,19 @@
 // safetyraise_kernel_attention_forward_noalloc: safetyraise_kernel_attention_forward
-// for callers that cannot allocate device memory (code under HIP graph
-// capture, tight serving loops).  It runs the same kernels; the call's
+// for callers that cannot allocate device memory (tight serving loops,
+// harnesses that forbid hipMalloc).  Like the ordinary entry point it refuses
+// calls while the stream is capturing a HIP graph: the sequences' lengths and
+// page lists advance on the host when a call is made, so a replayed call
+// would not advance them.  It runs the same kernels; the call's
 // scratch (the split-K partial records of the decode and verify kernels, the
 // per-row RoPE table of the verify and prefill kernels) comes from a fixed
 // file-scope device array instead of the context's grow-on-demand buffers,
 // and no staging is needed because the inputs must be device pointers.
 //
-// The array is one per GPU the library runs on, held until the process ends.
+// The array is one per GPU the library runs on: it is part of the library's
+// code object, so it is reserved on a GPU (64 MiB of device memory) as soon
+// as that code object is loaded there, i.e. at the library's first kernel
+// launch on that GPU, whether or not this entry point is ever called, and it
+// is held until the process ends.
 // Its device address is looked up once per device (hipGetSymbolAddress, with
 // that device current) and kept; host code never passes the array's name to
 // a kernel, only that address.  Every call on a GPU shares its array: calls
@@ -99,6 +106,8 @@ using namespace sr;
 extern "C" SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_attention_forward_noalloc(
     safetyraise_kernel_context *context, const safetyraise_kernel_attention_args *args) {
     if (context == nullptr) return kInvalid;
+    const int32_t capture = refuse_under_capture(context, "attention_forward_noalloc");
+    if (capture != kOk) return capture;
     if (args == nullptr || args->struct_size < sizeof(safetyraise_kernel_attention_args)) {
         return fail(context, kInvalid, "attention args pointer or struct_size is invalid");
     }

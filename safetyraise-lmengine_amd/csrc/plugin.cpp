@@ -100,6 +100,21 @@ int32_t finish_call(Ctx *ctx, bool async) {
     return error_word_status(ctx, word);
 }
 
+int32_t refuse_under_capture(Ctx *ctx, const char *what) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &status) != hipSuccess) {
+        (void)hipGetLastError();  // the query's own error is not this call's
+        return kOk;
+    }
+    if (status == hipStreamCaptureStatusNone) return kOk;
+    std::string message = what;
+    message += " cannot be captured into a HIP graph: a call appends at the sequences' "
+               "current lengths and advances them and their page lists on the host when it is "
+               "made, so a replay would write the same cache positions again and never advance "
+               "them";
+    return fail(ctx, kInvalid, message.c_str());
+}
+
 int32_t report_pending_async(Ctx *ctx) {
     if (!ctx->async_pending) return kOk;
     uint32_t word = 0;
@@ -121,6 +136,7 @@ LaunchEvents timed_launch(const char *kernel) {
     KernelTimer *t = t_timer;
     if (t == nullptr) return {};
     if (t->used == t->records.size()) {
+        if (t->records.size() >= KernelTimer::kMaxRecords) return {};  // window full: untimed
         KernelTimer::Record r{kernel, nullptr, nullptr};
         if (hipEventCreate(&r.start) != hipSuccess) return {};
         if (hipEventCreate(&r.stop) != hipSuccess) {

@@ -64,6 +64,9 @@ struct KernelTimer {
         hipEvent_t start;
         hipEvent_t stop;
     };
+    // launches recorded per window at most (one event pair each); later
+    // launches of the window run untimed
+    static constexpr size_t kMaxRecords = 65536;
     bool enabled = false;
     std::vector<Record> records;  // events are reused after timing_reset
     size_t used = 0;
@@ -203,6 +206,9 @@ int32_t finish_call(Ctx *ctx, bool async);  // sync + sticky error check unless 
 // At the start of a synchronous call: waits for earlier ASYNC work, if any,
 // and reports the errors its kernels raised (as the header promises), so
 // that the error word the call reads at its end holds only its own bits.
+// INVALID_ARGUMENT when the context's stream is capturing a HIP graph: the
+// calls that advance host-side KV bookkeeping cannot be replayed.
+int32_t refuse_under_capture(Ctx *ctx, const char *what);
 int32_t report_pending_async(Ctx *ctx);
 // Synchronises the context stream and returns the sticky error word, cleared.
 int32_t take_error_word(Ctx *ctx, uint32_t *word);

@@ -280,3 +280,39 @@ def test_weights_without_columns_give_zeros(backend, rng, torch_mod, dtype):
             assert np.array_equal(O.linear(x, empty, dtype), np.zeros((rows, out), np.float32))
         finally:
             prepared.destroy()
+
+
+@pytest.mark.parametrize("rows,cols,out", [(9, 256, 130), (256, 128, 8200)])
+def test_inputs_above_the_bf16_range(backend, rng, torch_mod, rows, cols, out):
+    # finite f32 inputs above bf16's largest value (3.3895e38) round to
+    # infinity as bf16; the exact three-part split of x takes its first part
+    # from x clamped to that value, so products stay finite and exact.  Row
+    # tile kernel (9 rows) and the tiled product (256 rows); one large input
+    # per row, weights small powers of two times integers, so each output is
+    # one exact product (ref rounding) plus ordinary terms
+    torch = torch_mod
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    big = np.array([3.3896e38, 3.39e38, 3.4e38, np.finfo(np.float32).max], np.float32)
+    col = rng.integers(0, cols, size=rows)
+    x[np.arange(rows), col] = big[np.arange(rows) % 4] * np.where(np.arange(rows) % 3, 1, -1)
+    w = (rng.integers(-4, 5, size=(out, cols)) / 64.0).astype(np.float32)
+    bits = weight_bits(w, BF16)
+    prepared = backend.create_weight(bits, BF16)
+    try:
+        ref = O.linear(x, bits, BF16)
+        assert np.isfinite(ref).all()
+        host = backend.linear(prepared, x)
+        dx = torch.from_numpy(x).cuda()
+        dy = torch.zeros((rows, out), device="cuda")
+        backend.check(backend.lib.safetyraise_kernel_linear_device(
+            backend.context, prepared.handle, C.c_void_p(dx.data_ptr()), rows, cols,
+            C.c_void_p(dy.data_ptr()), rows, out), "linear_device")
+        backend.synchronize()
+        dev = dy.cpu().numpy()
+        mag = np.abs(x.astype(np.float64)) @ np.abs(widened(bits, BF16)).T
+        for got in (host, dev):
+            assert np.isfinite(got).all()
+            bad = np.abs(got.astype(np.float64) - ref) > 1e-6 * mag + 1e-4 * np.abs(ref)
+            assert not bad.any(), (rows, np.abs(got - ref).max())
+    finally:
+        prepared.destroy()

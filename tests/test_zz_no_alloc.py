@@ -137,3 +137,51 @@ def test_noalloc_rejects_host_pointers_and_oversized_calls(pkg, backend, torch_m
     assert pool.len(s) == 0
     del tq, tk, tp, to
     pool.destroy()
+
+
+def test_calls_under_graph_capture_are_refused(pkg, backend, torch_mod):
+    # a call advances the sequences' lengths and page lists on the host when
+    # it is made, so a captured call could not be replayed: both entry points
+    # refuse while the context's stream captures, before touching anything,
+    # and the sequence is unchanged and usable afterwards
+    torch = torch_mod
+    P = pkg.plugin
+    lib = backend.lib
+    pool = pkg.KvCache(backend, 8, 128, 64, 64, 1024, 2)
+    s = pool.open()
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    q = torch.randn((1, 32 * 128), generator=gen, device="cuda").bfloat16()
+    k = torch.randn((1, 8 * 128), generator=gen, device="cuda").bfloat16()
+    pos = torch.zeros((1, 3), dtype=torch.int32, device="cuda")
+    gq = torch.ones(128, device="cuda")
+    out = torch.zeros((1, 32 * 128), device="cuda")
+    a = make_args(pkg, pool, [s], [1], q, k, k, pos, out, gq, gq)
+    a.flags |= P.ASYNC
+    x = torch.zeros(4, device="cuda")
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    backend.set_stream(stream.cuda_stream)
+    try:
+        with torch.cuda.graph(graph, stream=stream):
+            x.add_(1.0)
+            st_plain = lib.safetyraise_kernel_attention_forward(backend.context, C.byref(a))
+            text = lib.safetyraise_kernel_last_error(backend.context).decode()
+            st_noalloc = lib.safetyraise_kernel_attention_forward_noalloc(backend.context,
+                                                                          C.byref(a))
+    finally:
+        backend.set_stream(None)
+    assert st_plain == P.STATUS_INVALID_ARGUMENT and st_noalloc == P.STATUS_INVALID_ARGUMENT
+    assert "graph" in text
+    assert pool.len(s) == 0
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(x, torch.ones(4, device="cuda"))
+    # outside capture the same call runs
+    a.flags &= ~P.ASYNC
+    backend.check(lib.safetyraise_kernel_attention_forward_noalloc(backend.context, C.byref(a)),
+                  "attention_forward_noalloc")
+    assert pool.len(s) == 1
+    assert torch.isfinite(out).all()
+    pool.destroy()
