@@ -69,6 +69,50 @@ def traffic_from_profiles(kernel_tag: str):
         return None
 
 
+def mfma_from_profiles(kernel_tag: str, kernels, launch_us: dict):
+    """MFMA use of the leg's kernels from the committed rocprofv3 SQ-counter
+    summary (profiles/<tag>_pmc.json): the counted MFMA busy fraction
+    (SQ_VALU_MFMA_BUSY_CYCLES over 4 SIMDs x CUs x elapsed cycles), the MFMA
+    FLOPs issued per launch (SQ_INSTS_VALU_MFMA_MOPS_* x 512, fixed by the
+    workload's shapes) and, with this run's launch durations, the issued rate
+    and the time those MFMAs take at the dense peak of their type."""
+    f = PROFILES / f"{kernel_tag}_pmc.json"
+    if not f.exists():
+        return None
+    try:
+        prof = json.loads(f.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    out = {"source": f"profiles/{kernel_tag}_pmc.json", "kernels": {}}
+    at_peak_us = run_us = 0.0
+    for prefix in kernels:
+        found = [(n, d) for n, d in prof.items() if n.startswith(prefix) and "mfma_util" in d]
+        if not found or prefix not in launch_us:
+            continue
+        name, d = found[0]
+        c = d["counters_mean_per_dispatch"]
+        f32_flops = 512 * c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0)
+        half_flops = d["mfma_flops_issued"] - f32_flops
+        us = launch_us[prefix]
+        peak_us = 1e6 * (f32_flops / (MFMA_F32_PEAK_TFS * 1e12)
+                         + half_flops / (MFMA_BF16_PEAK_TFS * 1e12))
+        at_peak_us += peak_us
+        run_us += us
+        out["kernels"][name] = {
+            "pmc_mfma_util": d["mfma_util"],
+            "mfma_flops_issued_per_launch": d["mfma_flops_issued"],
+            "issued_tflops_this_run": round(d["mfma_flops_issued"] / (us * 1e-6) / 1e12, 2),
+            "valu_non_mfma_per_mfma": d["valu_non_mfma_per_mfma"],
+            "lds_bank_conflict_frac": d["lds_bank_conflict_frac_of_lds_active"],
+        }
+    if not out["kernels"]:
+        return None
+    # the share of the kernels' time their MFMAs would take at the dense peak
+    # of each type (f32 157.3, fp16/bf16 2500 TFLOP/s)
+    out["issued_at_peak_frac_of_time"] = round(at_peak_us / run_us, 4)
+    return out
+
+
 def _load_roctx():
     """The ROCTx range API: `rocprofv3 --marker-trace` records the ranges, and
     without a profiler the calls do nothing.  None when the library is absent."""
@@ -450,6 +494,8 @@ def bench_prefill(args, torch, pkg, steps, warmup):
             "launch_us_mean": round(float(attn_us), 2),
             "flops_per_launch": int(step_flops // nchunk),
             "flops_per_step": int(step_flops),
+            "mfma_util": mfma_from_profiles("attn_prefill_qwen3_8b", [attn_name],
+                                            {attn_name: float(attn_us)}),
         },
         "kernels": kernels,
     }
@@ -732,18 +778,32 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
         "gflop_per_step_token_serial": round(flops / 1e9, 2),
         "gflop_per_step_chunked_form": round(chunked_form / 1e9, 2),
-        "dtype": "f32 (MFMA 16x16x4 f32, chunked WY form)",
+        # the state products run on split bf16 operands (hi + lo parts of every
+        # f32 operand, three bf16 MFMAs per product, exact products in f32);
+        # the state-independent prep on the f32 MFMA
+        "dtype": "f32 results: chunked WY form, prep on v_mfma_f32_16x16x4f32, scan on "
+                 "split-bf16 operands (v_mfma_f32_16x16x32_bf16, hi/lo parts)",
         "roofline": {
-            "bound": "mfma", "achieved": round(chunk_tf, 3), "peak": MFMA_F32_PEAK_TFS,
-            "unit": "TFLOP/s", "frac": round(chunk_tf / MFMA_F32_PEAK_TFS, 4),
-            "frac_token_serial": round(serial_tf / MFMA_F32_PEAK_TFS, 4),
+            # achieved: the reference's own (token-serial) f32 work over the
+            # chunked kernels' time, against the f32 matrix peak: the arithmetic
+            # the path must reproduce, whatever form computes it
+            "bound": "mfma", "achieved": round(serial_tf, 3), "peak": MFMA_F32_PEAK_TFS,
+            "unit": "TFLOP/s", "frac": round(serial_tf / MFMA_F32_PEAK_TFS, 4),
+            "flops_counted": "token-serial: 7 Dk Dv per (row, value head)",
+            "chunked_form_tflops": round(chunk_tf, 3),
+            "chunked_form_frac": round(chunk_tf / MFMA_F32_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("gdn_prefill_qwen35"),
             "kernel": "gdn_chunk_prep_kernel<ConvK<4>, true> + gdn_chunk_scan_kernel (the "
                       "call's chunked form, its prep with two workgroups per record: sum of the "
                       "two kernels' mean durations)",
             "launch_us_mean": round(float(chunk_us), 2),
-            "flops_per_launch": int(chunked_form / nchunk),
-            "flops_per_step": int(chunked_form),
+            "flops_per_launch": int(flops / nchunk),
+            "flops_per_step": int(flops),
+            "chunked_form_flops_per_step": int(chunked_form),
+            "mfma_util": mfma_from_profiles(
+                "gdn_prefill_qwen35", ["gdn_chunk_prep_kernel", "gdn_chunk_scan_kernel"],
+                {n: float(kernels[n]["us"]) for n in ("gdn_chunk_prep_kernel",
+                                                      "gdn_chunk_scan_kernel")}),
         },
         "kernels": kernels,
     }
@@ -758,8 +818,10 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
 
 
 def cpu_baseline_gdn(pool, ids_c, qkv_dev, layer, hk, hv, dk, dv, K, nseq, rows, work, unit):
-    """CPU oracle (1 thread: the reference's row loop is serial) on `nseq` sequences x
-    `rows` rows of the same layer shape, from the GPU pool's current state."""
+    """CPU oracle on `nseq` sequences x `rows` rows of the same layer shape, from
+    the GPU pool's current state: 1 thread (the reference's row loop is
+    serial) and all cores (min(cores, 16) threads, value heads split over
+    them: the same arithmetic per head)."""
     from oracle import pyoracle as O
 
     rng = np.random.default_rng(7)
@@ -768,23 +830,42 @@ def cpu_baseline_gdn(pool, ids_c, qkv_dev, layer, hk, hv, dk, dv, K, nseq, rows,
     a_log = layer["a_log"].cpu().numpy()
     dt_bias = layer["dt_bias"].cpu().numpy()
     norm = layer["norm"].cpu().numpy()
-    t = 0.0
+    from concurrent.futures import ThreadPoolExecutor
+
+    nthreads = min(os.cpu_count() or 1, 16)
+    inputs = []
     for i in range(nseq):
         m, hst = pool.read(ids_c[i])
-        qkv = rng.standard_normal((rows, C_)).astype(np.float32)
-        z = rng.standard_normal((rows, hv * dv)).astype(np.float32)
-        a = rng.standard_normal((rows, hv)).astype(np.float32)
-        b = rng.standard_normal((rows, hv)).astype(np.float32)
-        t0 = time.perf_counter()
+        inputs.append((m, hst, rng.standard_normal((rows, C_)).astype(np.float32),
+                       rng.standard_normal((rows, hv * dv)).astype(np.float32),
+                       rng.standard_normal((rows, hv)).astype(np.float32),
+                       rng.standard_normal((rows, hv)).astype(np.float32)))
+
+    def one(item, threads):
+        m, hst, qkv, z, a, b = item
         O.gdn_rows(qkv, z, a, b, a_log, dt_bias, conv, K, norm, 1e-6, key_heads=hk,
-                   value_heads=hv, key_dim=dk, value_dim=dv, history=hst, state=m)
-        t += time.perf_counter() - t0
+                   value_heads=hv, key_dim=dk, value_dim=dv, history=hst.copy(),
+                   state=m.copy(), threads=threads)
+
+    t0 = time.perf_counter()
+    for item in inputs:
+        one(item, 1)
+    t = time.perf_counter() - t0
+    # all cores: the sequences side by side (ctypes releases the GIL), each
+    # with its value heads split over its share of the threads
+    per_seq = max(1, nthreads // nseq)
+    with ThreadPoolExecutor(min(nseq, nthreads)) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(lambda item: one(item, per_seq), inputs))
+        tm = time.perf_counter() - t0
     scale = 1e9 if unit in ("GB/s", "GFLOP/s") else 1.0
     per_item = work / nseq if unit == "GB/s" else work
     return {"value": round(per_item * nseq / t / scale, 3), "unit": unit, "cores": 1,
             "kind": "port",
             "sample": f"{nseq} sequence(s) x {rows} row(s) of the same layer shape, f32 oracle",
-            "ms": round(t * 1e3, 2)}
+            "ms": round(t * 1e3, 2),
+            "all_cores": {"value": round(per_item * nseq / tm / scale, 3),
+                          "cores": min(nthreads, nseq * per_seq), "ms": round(tm * 1e3, 2)}}
 
 
 # Qwen3-8B decoder layer projections (out, in): q, k, v, o, gate, up, down
@@ -956,9 +1037,16 @@ def bench_linear_prefill(args, torch, pkg, steps, warmup, rows=2048):
             "flops_per_launch": int(3 * launch_flops),
             "exact_product_tflops_per_launch": round(launch_flops / (gemm_us * 1e-6) / 1e12, 2),
             "fp32_matrix_peak": MFMA_F32_PEAK_TFS,
+            "mfma_util": mfma_from_profiles(
+                "linear_prefill_qwen3_8b", [k for k in ("linear_gemm_wide_kernel",
+                                                        "linear_gemm_kernel") if k in kernels],
+                {k: float(kernels[k]["us"]) for k in ("linear_gemm_wide_kernel",
+                                                      "linear_gemm_kernel") if k in kernels}),
         },
         "kernels": kernels,
     }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_linear_prefill(xs[0])
     for w in weights:
         w.destroy()
     backend.close()
@@ -983,6 +1071,36 @@ def cpu_baseline_linear(weight, x_dev, rows):
             "sample": "q projection (4096 x 4096 bf16) for 4 rows, f32 oracle (the reference "
                       "plugin's loop), scaled to the 16-row call",
             "ms": round(t * 1e3, 2)}
+
+
+def cpu_baseline_linear_prefill(x_dev):
+    """The oracle's linear (the reference CPU plugin's loop) on the q
+    projection (4096 x 4096 bf16): 4 rows on 1 thread, and 4 rows per thread on
+    min(cores, 16) threads at once (ctypes releases the GIL), as GFLOP/s of the
+    f32 product (2 rows x out x in per call, the GPU figure's count)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from oracle import pyoracle as O
+
+    out_f, in_f = LINEAR_SHAPES[0]
+    rng = np.random.default_rng(12)
+    bits = (rng.integers(0, 1 << 16, size=(out_f, in_f), dtype=np.uint32) & 0x3fff).astype(np.uint16)
+    nthreads = min(os.cpu_count() or 1, 16)
+    x = x_dev[:4 * nthreads].cpu().numpy()
+    t0 = time.perf_counter()
+    O.linear(x[:4], bits, 3)
+    t1 = time.perf_counter() - t0
+    with ThreadPoolExecutor(nthreads) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(lambda i: O.linear(x[4 * i:4 * i + 4], bits, 3), range(nthreads)))
+        tm = time.perf_counter() - t0
+    flops = 2 * 4 * out_f * in_f
+    return {"value": round(flops / t1 / 1e9, 3), "unit": "GFLOP/s", "cores": 1, "kind": "port",
+            "sample": "q projection (4096 x 4096 bf16) for 4 rows per thread, f32 oracle (the "
+                      "reference plugin's loop)",
+            "ms": round(t1 * 1e3, 2),
+            "all_cores": {"value": round(nthreads * flops / tm / 1e9, 3), "cores": nthreads,
+                          "ms": round(tm * 1e3, 2)}}
 
 
 def bench_verify(args, torch, pkg, steps, warmup, rows=5):

@@ -82,6 +82,9 @@ def lib() -> C.CDLL:
         L.sro_gdn_rows.restype = i
         L.sro_gdn_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, _f32p, _f32p, _f32p, sz, _f32p,
                                    f, sz, sz, sz, sz, _f32p, _f32p, _f32p]
+        L.sro_gdn_rows_mt.restype = i
+        L.sro_gdn_rows_mt.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, _f32p, _f32p, _f32p, sz,
+                                      _f32p, f, sz, sz, sz, sz, _f32p, _f32p, _f32p, i]
         _lib = L
     return _lib
 
@@ -239,15 +242,18 @@ def attention_rows(q_raw, k_raw, v_raw, positions, cache: KvCache, *, heads: int
 
 def gdn_rows(qkv, z, a, b, a_log, dt_bias, conv_weight, kernel: int, norm, eps: float, *,
              key_heads: int, value_heads: int, key_dim: int, value_dim: int,
-             history: np.ndarray, state: np.ndarray) -> np.ndarray:
+             history: np.ndarray, state: np.ndarray, threads: int = 1) -> np.ndarray:
     q = f32(qkv)
     rows = q.shape[0]
     out = np.empty((rows, value_heads * value_dim), np.float32)
     assert history.dtype == np.float32 and state.dtype == np.float32
-    _ok(lib().sro_gdn_rows(q.ravel(), f32(z).ravel(), f32(a).ravel(), f32(b).ravel(), rows,
-                           f32(a_log), f32(dt_bias), f32(conv_weight).ravel(), kernel, f32(norm),
-                           eps, key_heads, value_heads, key_dim, value_dim,
-                           history.reshape(-1), state.reshape(-1), out.ravel()), "gdn_rows")
+    args = (q.ravel(), f32(z).ravel(), f32(a).ravel(), f32(b).ravel(), rows, f32(a_log),
+            f32(dt_bias), f32(conv_weight).ravel(), kernel, f32(norm), eps, key_heads,
+            value_heads, key_dim, value_dim, history.reshape(-1), state.reshape(-1), out.ravel())
+    if threads > 1:
+        _ok(lib().sro_gdn_rows_mt(*args, threads), "gdn_rows")
+    else:
+        _ok(lib().sro_gdn_rows(*args), "gdn_rows")
     return out
 
 

@@ -389,17 +389,16 @@ int sro_causal_conv_silu(const float *input, size_t channels, const float *weigh
 
 /* ---------------- gated_delta_step (src/model/math.rs:190-239) ---------------- */
 
-int sro_gated_delta_step(const float *qkv, const float *a, const float *b,
-                         const float *a_log, const float *dt_bias, size_t key_heads,
-                         size_t value_heads, size_t key_dim, size_t value_dim, float *state,
-                         float *output) {
-    if (key_heads == 0 || value_heads % key_heads != 0) {
-        return SRO_INVALID; /* :201-210 */
-    }
+/* value heads h0..h1-1 of one gated_delta_step: every head's arithmetic
+ * depends only on its own state rows and the row's q/k of its key head */
+static void delta_heads(const float *qkv, const float *a, const float *b, const float *a_log,
+                        const float *dt_bias, size_t key_heads, size_t value_heads,
+                        size_t key_dim, size_t value_dim, size_t h0, size_t h1, float *state,
+                        float *output) {
     const size_t key_width = key_heads * key_dim;
     const size_t key_groups = value_heads / key_heads;
     const float query_scale = 1.0f / sqrtf((float)key_dim); /* :213 */
-    for (size_t h = 0; h < value_heads; ++h) {
+    for (size_t h = h0; h < h1; ++h) {
         const size_t start = h / key_groups * key_dim; /* :215 */
         const float *q = qkv + start;
         const float *k = qkv + key_width + start;
@@ -428,6 +427,17 @@ int sro_gated_delta_step(const float *qkv, const float *a, const float *b,
             output[h * value_dim + v] = read * query_scale;
         }
     }
+}
+
+int sro_gated_delta_step(const float *qkv, const float *a, const float *b,
+                         const float *a_log, const float *dt_bias, size_t key_heads,
+                         size_t value_heads, size_t key_dim, size_t value_dim, float *state,
+                         float *output) {
+    if (key_heads == 0 || value_heads % key_heads != 0) {
+        return SRO_INVALID; /* :201-210 */
+    }
+    delta_heads(qkv, a, b, a_log, dt_bias, key_heads, value_heads, key_dim, value_dim, 0,
+                value_heads, state, output);
     return SRO_OK;
 }
 
@@ -525,6 +535,95 @@ int sro_gdn_rows(const float *qkv, const float *z, const float *a, const float *
         if (status != SRO_OK) break;
         for (size_t i = 0; i < width; ++i) {
             o[i] *= sro_silu(z[row * width + i]); /* :738-740 */
+        }
+    }
+done:
+    free(conv);
+    free(recurrent);
+    return status;
+}
+
+/* sro_gdn_rows with the value heads split over threads (the CPU baseline's
+ * all-cores figure).  The conv of every row runs first (it reads no state);
+ * then each thread runs the delta rule, norm and gate of its heads over all
+ * rows.  Every head's operations and their order are those of sro_gdn_rows,
+ * so the results are identical to it bit for bit. */
+typedef struct {
+    const float *conv, *z, *a, *b, *a_log, *dt_bias, *norm;
+    size_t rows, channels, key_heads, value_heads, key_dim, value_dim, h0, h1;
+    float eps;
+    float *state, *recurrent, *out;
+    int status;
+} gdn_job;
+
+static void *gdn_worker(void *arg) {
+    gdn_job *j = (gdn_job *)arg;
+    const size_t width = j->value_heads * j->value_dim;
+    for (size_t row = 0; row < j->rows; ++row) {
+        float *rec = j->recurrent + row * width;
+        delta_heads(j->conv + row * j->channels, j->a + row * j->value_heads,
+                    j->b + row * j->value_heads, j->a_log, j->dt_bias, j->key_heads,
+                    j->value_heads, j->key_dim, j->value_dim, j->h0, j->h1, j->state, rec);
+        const size_t off = j->h0 * j->value_dim, n = (j->h1 - j->h0) * j->value_dim;
+        float *o = j->out + row * width + off;
+        const int st = sro_rms_norm(rec + off, n, j->norm, j->value_dim, j->eps, 0, o);
+        if (st != SRO_OK) {
+            j->status = st;
+            return NULL;
+        }
+        for (size_t i = 0; i < n; ++i) {
+            o[i] *= sro_silu(j->z[row * width + off + i]);
+        }
+    }
+    return NULL;
+}
+
+int sro_gdn_rows_mt(const float *qkv, const float *z, const float *a, const float *b,
+                    size_t rows, const float *a_log, const float *dt_bias,
+                    const float *conv_weight, size_t kernel, const float *norm, float eps,
+                    size_t key_heads, size_t value_heads, size_t key_dim, size_t value_dim,
+                    float *history, float *state, float *out, int nthreads) {
+    if (key_heads == 0 || value_heads % key_heads != 0) {
+        return SRO_INVALID;
+    }
+    if (nthreads <= 1) {
+        return sro_gdn_rows(qkv, z, a, b, rows, a_log, dt_bias, conv_weight, kernel, norm, eps,
+                            key_heads, value_heads, key_dim, value_dim, history, state, out);
+    }
+    if ((size_t)nthreads > value_heads) nthreads = (int)value_heads;
+    if (nthreads > 256) nthreads = 256;
+    const size_t channels = 2 * key_heads * key_dim + value_heads * value_dim;
+    const size_t width = value_heads * value_dim;
+    float *conv = (float *)malloc(rows * channels * sizeof(float) + 1);
+    float *recurrent = (float *)malloc(rows * width * sizeof(float) + 1);
+    int status = SRO_OK;
+    if (conv == NULL || recurrent == NULL) {
+        status = SRO_NOMEM;
+        goto done;
+    }
+    for (size_t row = 0; row < rows; ++row) {
+        status = sro_causal_conv_silu(qkv + row * channels, channels, conv_weight, kernel,
+                                      history, conv + row * channels);
+        if (status != SRO_OK) goto done;
+    }
+    {
+        pthread_t threads[256];
+        gdn_job jobs[256];
+        for (int t = 0; t < nthreads; ++t) {
+            gdn_job j = {conv, z, a, b, a_log, dt_bias, norm, rows, channels, key_heads,
+                         value_heads, key_dim, value_dim,
+                         value_heads * (size_t)t / (size_t)nthreads,
+                         value_heads * (size_t)(t + 1) / (size_t)nthreads, eps, state,
+                         recurrent, out, SRO_OK};
+            jobs[t] = j;
+            if (pthread_create(&threads[t], NULL, gdn_worker, &jobs[t]) != 0) {
+                gdn_worker(&jobs[t]);
+                threads[t] = 0;
+            }
+        }
+        for (int t = 0; t < nthreads; ++t) {
+            if (threads[t] != 0) pthread_join(threads[t], NULL);
+            if (jobs[t].status != SRO_OK) status = jobs[t].status;
         }
     }
 done:

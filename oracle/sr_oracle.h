@@ -92,6 +92,14 @@ int sro_gdn_rows(const float *qkv, const float *z, const float *a, const float *
                  size_t key_heads, size_t value_heads, size_t key_dim, size_t value_dim,
                  float *history, float *state, float *out);
 
+/* sro_gdn_rows with value heads split over nthreads threads; bit-identical
+ * results (test infrastructure: the CPU baseline's all-cores figure). */
+int sro_gdn_rows_mt(const float *qkv, const float *z, const float *a, const float *b,
+                    size_t rows, const float *a_log, const float *dt_bias,
+                    const float *conv_weight, size_t kernel, const float *norm, float eps,
+                    size_t key_heads, size_t value_heads, size_t key_dim, size_t value_dim,
+                    float *history, float *state, float *out, int nthreads);
+
 /* ABI v1 linear (native/cpu/safetyraise_cpu.c:203-239): output[r][o] =
  * sum over c, in order, of input[r][c] * weight[o][c] in f32, with the weight
  * widened exactly from its dtype (1 = f32, 2 = f16 as :47-78, 3 = bf16 by

@@ -451,6 +451,31 @@ def test_gdn_rows_match_f64_brute_force(hk, hv, dk, dv, K):
     close(hist, h64, 0.0, 0.0)
 
 
+@pytest.mark.parametrize("threads", [2, 3, 8])
+def test_gdn_rows_threaded_equals_serial_bit_for_bit(threads):
+    # the CPU baseline's all-cores GDN figure splits value heads over threads;
+    # each head's operations are those of the serial loop, so outputs, state
+    # and history are identical
+    hk, hv, dk, dv, K, rows = 2, 6, 16, 8, 4, 9
+    C = 2 * hk * dk + hv * dv
+    qkv = RNG.standard_normal((rows, C)).astype(np.float32)
+    z = RNG.standard_normal((rows, hv * dv)).astype(np.float32)
+    a = RNG.standard_normal((rows, hv)).astype(np.float32)
+    b = RNG.standard_normal((rows, hv)).astype(np.float32)
+    a_log = (0.1 * RNG.standard_normal(hv)).astype(np.float32)
+    dt = (0.1 * RNG.standard_normal(hv)).astype(np.float32)
+    w = (RNG.standard_normal((C, K)) / 2).astype(np.float32)
+    norm = (1 + 0.1 * RNG.standard_normal(dv)).astype(np.float32)
+    hist = (0.5 * RNG.standard_normal((C, K - 1))).astype(np.float32)
+    state = (0.02 * RNG.standard_normal((hv, dv, dk))).astype(np.float32)
+    h1, s1, h2, s2 = hist.copy(), state.copy(), hist.copy(), state.copy()
+    kw = dict(key_heads=hk, value_heads=hv, key_dim=dk, value_dim=dv)
+    o1 = O.gdn_rows(qkv, z, a, b, a_log, dt, w, K, norm, 1e-6, history=h1, state=s1, **kw)
+    o2 = O.gdn_rows(qkv, z, a, b, a_log, dt, w, K, norm, 1e-6, history=h2, state=s2,
+                    threads=threads, **kw)
+    assert np.array_equal(o1, o2) and np.array_equal(s1, s2) and np.array_equal(h1, h2)
+
+
 # ---------------------------------------------------------------------------
 # ABI v1 linear (native/cpu/safetyraise_cpu.c:203-239)
 # ---------------------------------------------------------------------------
