@@ -47,8 +47,9 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="decode",
-                   choices=["decode", "prefill", "verify", "gdn-decode", "gdn-prefill", "linear",
-                            "linear-prefill", "copy"])
+                   choices=["decode", "prefill", "verify", "verify-qwen3.5", "gdn-decode",
+                            "gdn-prefill", "linear", "linear-prefill", "copy"])
+    p.add_argument("--rows", type=int, default=5, help="verify rows per sequence (1 + drafts)")
     p.add_argument("--no-prefill", action="store_true",
                    help="decode workload only (skip the prefill figure of the same line)")
     p.add_argument("--prefill-steps", type=int, default=10)
@@ -1103,7 +1104,17 @@ def cpu_baseline_linear_prefill(x_dev):
                           "ms": round(tm * 1e3, 2)}}
 
 
-def bench_verify(args, torch, pkg, steps, warmup, rows=5):
+# verify shapes: (heads, kv heads, head_dim, rotary_dim, theta, gated)
+VERIFY_SHAPES = {
+    # BASELINE config 5
+    "qwen3-32b": (64, 8, 128, 128, 1e6, False),
+    # Qwen3.5 full attention (the model the reference's MTP runs,
+    # src/model/mtp.rs:110-112): q/gate interleaved, partial rotary 64, theta 1e7
+    "qwen3.5": (16, 2, 256, 64, 1e7, True),
+}
+
+
+def bench_verify(args, torch, pkg, steps, warmup, rows=5, shape="qwen3-32b"):
     """long-context MTP speculative-verify attention, Qwen3-32B
     shape: 64 Q / 8 KV heads, head_dim 128, 1 + 4 draft rows per sequence (row j
     sees 131072 + j + 1 keys), batch 4, context 131072, paged bf16 KV in 16-token
@@ -1111,8 +1122,12 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
     page_order_seed), so no two consecutive pages of a sequence are adjacent
     except by chance.  One step = one verify call; the drafts are truncated away
     afterwards (the next step verifies at the same context).  Inputs ~N(0,1) are
-    taken as normalised (no QK-norm); RoPE is applied as part of the fused path."""
-    heads, kvh, dim, nseq, ctx_len, page = 64, 8, 128, 4, 131072, 16
+    taken as normalised (no QK-norm); RoPE is applied as part of the fused path.
+    shape "qwen3.5": the same workload at the Qwen3.5 full-attention geometry
+    (16 Q / 2 KV heads, head_dim 256, gated); rows 9 = 1 + 8 drafts, the
+    engine's cap (src/engine/speculative.rs:12)."""
+    heads, kvh, dim, rotary, theta, gated = VERIFY_SHAPES[shape]
+    nseq, ctx_len, page = 4, 131072, 16
     backend = pkg.NativeBackend.load()
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -1129,7 +1144,8 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
         pool.append(s_, kfull, vfull, flags=pkg.ASYNC)
     backend.synchronize()
     del kfull, vfull
-    q = torch.randn((nseq * rows, heads * dim), generator=gen, device="cuda")
+    qw = heads * dim * (2 if gated else 1)
+    q = torch.randn((nseq * rows, qw), generator=gen, device="cuda")
     k = torch.randn((nseq * rows, kvh * dim), generator=gen, device="cuda")
     v = torch.randn((nseq * rows, kvh * dim), generator=gen, device="cuda")
     out = torch.empty((nseq * rows, heads * dim), device="cuda")
@@ -1138,9 +1154,9 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
     P = pkg.plugin
     a = P.AttentionArgs()
     a.struct_size = C.sizeof(P.AttentionArgs)
-    a.flags = P.DEVICE_POINTERS | P.ASYNC | P.MROPE_INTERLEAVED
-    a.heads, a.kv_heads, a.head_dim, a.rotary_dim = heads, kvh, dim, dim
-    a.eps, a.rope_theta = 1e-6, 1e6
+    a.flags = P.DEVICE_POINTERS | P.ASYNC | P.MROPE_INTERLEAVED | (P.GATED if gated else 0)
+    a.heads, a.kv_heads, a.head_dim, a.rotary_dim = heads, kvh, dim, rotary
+    a.eps, a.rope_theta = 1e-6, theta
     a.num_seqs = nseq
     a.seq_ids = (C.c_uint32 * nseq)(*ids)
     a.seq_rows = (C.c_uint32 * nseq)(*([rows] * nseq))
@@ -1194,10 +1210,15 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
     flops = nseq * heads * 4 * dim * keys
     gbs = nbytes / (ms * 1e-3) / 1e9
     achieved = nbytes / (call_us * 1e-6) / 1e9
+    workload = ("qwen3-32b MTP verify attention (BASELINE config 5): 64 Q / 8 KV heads, "
+                "d 128, 1 + 4 rows, batch 4, context 131072, 16-token pages in a random "
+                "permutation of the pool") if shape == "qwen3-32b" else (
+        f"{shape} MTP verify attention: {heads} Q / {kvh} KV heads, d {dim}, gated, rotary "
+        f"{rotary}, 1 + {rows - 1} rows ({-(-rows // (64 // (heads // kvh)))} row slice(s) of "
+        f"at most 64 query vectors), batch 4, context 131072, 16-token pages in a random "
+        f"permutation of the pool")
     result = {
-        "workload": "qwen3-32b MTP verify attention (BASELINE config 5): 64 Q / 8 KV heads, "
-                    "d 128, 1 + 4 rows, batch 4, context 131072, 16-token pages in a random "
-                    "permutation of the pool",
+        "workload": workload,
         "value": round(gbs, 2), "unit": "GB/s",
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
@@ -1206,14 +1227,15 @@ def bench_verify(args, torch, pkg, steps, warmup, rows=5):
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles("attn_verify_qwen3_32b"),
-            "kernel": "attn_verify_kernel<128>",
+            "traffic": (traffic_from_profiles("attn_verify_qwen3_32b")
+                        if shape == "qwen3-32b" else None),
+            "kernel": f"attn_verify_kernel<{dim}>",
             "launch_us_mean": round(float(call_us), 2),
             "bytes_per_launch": int(nbytes),
         },
         "kernels": kernels,
     }
-    if not args.no_cpu:
+    if not args.no_cpu and shape == "qwen3-32b":
         result["cpu_baseline"] = cpu_baseline_verify(pool, ids[0], q, k, v, pos, heads, kvh, dim,
                                                      rows, ctx_len)
     pool.destroy()
@@ -1289,12 +1311,17 @@ def main():
         if not args.no_prefill:
             result["prefill"] = bench_prefill(args, torch, pkg, args.prefill_steps, 2)
             result["verify"] = bench_verify(args, torch, pkg, 30, 10)
+            result["verify"]["qwen3.5_d256"] = {
+                f"rows_{r}": bench_verify(args, torch, pkg, 30, 10, rows=r, shape="qwen3.5")
+                for r in (5, 9)}
             result["gdn_decode"] = bench_gdn_decode(args, torch, pkg, 20, 3)
             result["gdn_prefill"] = bench_gdn_prefill(args, torch, pkg, 10, 2)
             result["linear"] = bench_linear(args, torch, pkg, 50, 5)
             result["linear"]["prefill_rows"] = bench_linear_prefill(args, torch, pkg, 3, 1)
-    elif args.workload == "verify":
-        result = bench_verify(args, torch, pkg, args.steps, args.warmup)
+    elif args.workload in ("verify", "verify-qwen3.5"):
+        shape = "qwen3-32b" if args.workload == "verify" else "qwen3.5"
+        result = bench_verify(args, torch, pkg, args.steps, args.warmup, rows=args.rows,
+                              shape=shape)
         result = {"metric": "MTP verify attention GB/s", "n_gpus": 1, "higher_is_better": True,
                   "scaling": "weak", "vs_baseline": None, "data": "synthetic",
                   "config": {"workload": result.pop("workload")}, **result}

@@ -740,11 +740,111 @@ struct LdsRope {
     }
 };
 
+// q_operands at D = 256: a lane's 128 q values, its 128 norm weights and
+// 128 RoPE values held at once would exceed the 256 registers of a wave that
+// shares its SIMD.  Pass 1 streams q in for the sum of squares (the same
+// partial sums in the same order as q_operands); pass 2 reads each 8-dim
+// step again with its RoPE partner (dims i and i + rotary_dim/2 sit in the
+// same lane, steps st and st + rotary_dim/32) and the pair's weights and
+// (cos, sin), by address, so that no register array is indexed at run time.
+// Every output is the same expression on the same values as in q_operands.
+template <int D, class Rope>
+__device__ __forceinline__ void q_operands_two_pass(const QArgs &p, size_t qbase, uint32_t call_row,
+                                                    int h, f16x8 (&qop)[D / 16],
+                                                    const Rope *rope) {
+    constexpr int NS = D / 16;
+    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
+    const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
+    const uint32_t half = p.rotary_dim / 2;
+    const uint32_t hsteps = p.rotary_dim / 32;
+    Rope cs;
+    if constexpr (std::is_same<Rope, GlobalRope>::value) cs.row = p.rope_cs + (size_t)call_row * half;
+    else cs = *rope;
+    auto load8 = [&](uint32_t st, float (&x)[8]) __attribute__((always_inline)) {
+        if (bf16_in) {
+            const u32x4 w = *(const u32x4 *)((const uint16_t *)p.q + qbase + 16 * st + 8 * h);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = bf16_elem(w, j);
+        } else {
+            const size_t off = qbase + 16 * st + 8 * h;
+            const float4 a = *(const float4 *)((const float *)p.q + off);
+            const float4 c = *(const float4 *)((const float *)p.q + off + 4);
+            x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+            x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+        }
+    };
+    float inv = 1.0f;
+    if (qk_norm) {
+        float part[8];
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            float x[8];
+            load8(st, x);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part[j] = st == 0 ? x[j] * x[j] : part[j] + x[j] * x[j];
+        }
+        float ss = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+        ss = xhalf_sum(ss);
+        const float variance = ss / (float)D;
+        if (!isfinite(variance) && (threadIdx.x & 63) == 0) {
+            atomicOr(p.err_word, kErrNonFiniteVariance);
+        }
+        inv = 1.0f / sqrtf(variance + p.eps);
+    }
+    // x of step st, normalised as q_operands does it
+    auto normed8 = [&](uint32_t st, float (&x)[8]) __attribute__((always_inline)) {
+        load8(st, x);
+        if (qk_norm) {
+            const f32x4 w0 = *(const f32x4 *)(p.q_norm + 16 * st + 8 * h);
+            const f32x4 w1 = *(const f32x4 *)(p.q_norm + 16 * st + 8 * h + 4);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = x[j] * inv * ((j < 4 ? w0[j] : w1[j - 4]) + norm_add);
+        }
+    };
+    const float qscale = (1.0f / sqrtf((float)D)) * kLog2e;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        float x[8];
+        normed8(st, x);
+        const uint32_t ust = (uint32_t)st;
+        if (ust < 2 * hsteps) {
+            // rotated: left half (st < hsteps) or right half of a pair
+            const bool left = ust < hsteps;
+            const uint32_t pst = left ? ust + hsteps : ust - hsteps;  // the partner step
+            const uint32_t lst = left ? ust : pst;                     // the pair's (cos, sin) step
+            float y[8];
+            normed8(pst, y);
+#pragma unroll
+            for (int j2 = 0; j2 < 4; ++j2) {
+                const f32x4 cc = cs.pairs(16 * lst + 8 * h + 2 * j2);
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int j = 2 * j2 + k;
+                    const float c = k ? cc.z : cc.x;
+                    const float sn = k ? cc.w : cc.y;
+                    // left:  x[st] * cos - x[st + hsteps] * sin
+                    // right: x[st] * cos + x[st - hsteps] * sin
+                    x[j] = left ? x[j] * c - y[j] * sn : x[j] * c + y[j] * sn;
+                }
+            }
+        }
+        f32x8 v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = x[j] * qscale;
+        qop[st] = __builtin_convertvector(v, f16x8);
+    }
+}
+
 template <int D, class Rope = GlobalRope>
 __device__ __forceinline__ void q_operands(const QArgs &p, size_t qbase, uint32_t call_row,
                                            int h, int lane, f16x8 (&qop)[D / 16],
                                            const Rope *rope = nullptr) {
     constexpr int NS = D / 16;
+    if constexpr (D > 128) {
+        q_operands_two_pass<D>(p, qbase, call_row, h, qop, rope);
+        return;
+    }
     const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
     const bool qk_norm = (p.flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const float norm_add = (p.flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
@@ -941,23 +1041,29 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 
 // Byte offset of lane's transposing reads in a V tile, per 32-column tile
-// (k-step 0, first read; the other reads add 16 st and 8 rows).
-template <int D>
-__device__ __forceinline__ void pv_rows_offsets(int lane, uint32_t (&off)[D / 32]) {
-    static_assert(D == 128, "unit index: 16 units per row, 4 column tiles");
+// (k-step 0, first read; the other reads add 16 st and 8 rows): column tiles
+// tile0 .. tile0 + NT - 1 of a row-major [64 keys][D] tile (D = 128: 16
+// units of 16 bytes per row, 4 column tiles; D = 256: 32 units, 8 column
+// tiles, read NT = 4 at a time by the two halves of the output dims).  The
+// stored unit of logical unit c of key row r is c ^ ((r & 3) << 2) (v_swz),
+// and the 4 rows a lane reads have r & 3 = s / 4, so the XOR stays inside the
+// lane's column tile's four units.
+template <int D, int NT = D / 32>
+__device__ __forceinline__ void pv_rows_offsets(int lane, uint32_t (&off)[NT], uint32_t tile0 = 0) {
+    static_assert(D == 128 || D == 256, "row-major V tiles of 128 or 256 dims");
     const uint32_t s = lane & 15, g = lane >> 4;
     const uint32_t row = 4 * (g >> 1) + (s >> 2);
 #pragma unroll
-    for (int tt = 0; tt < D / 32; ++tt) {
-        const uint32_t unit = (((uint32_t)tt ^ (s >> 2)) << 2) | ((g & 1) << 1) | ((s >> 1) & 1);
+    for (int tt = 0; tt < NT; ++tt) {
+        const uint32_t unit = (((tile0 + (uint32_t)tt) ^ (s >> 2)) << 2) | ((g & 1) << 1) |
+                              ((s >> 1) & 1);
         off[tt] = row * (D * 2) + unit * 16 + (s & 1) * 8;
     }
 }
 
-template <int D>
-__device__ __forceinline__ void pv_tile_rows(const unsigned char *vt, const uint32_t (&off)[D / 32],
-                                             const f16x8 (&pop)[4], f32x16 (&oacc)[D / 32]) {
-    constexpr int NT = D / 32;
+template <int D, int NT = D / 32>
+__device__ __forceinline__ void pv_tile_rows(const unsigned char *vt, const uint32_t (&off)[NT],
+                                             const f16x8 (&pop)[4], f32x16 (&oacc)[NT]) {
     typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
     auto v_frag = [&](int tt, int st) __attribute__((always_inline)) -> f16x8 {
         const unsigned char *b = vt + off[tt] + st * 16 * (D * 2);
@@ -1528,12 +1634,20 @@ hipError_t launch_d(hipStream_t stream, PrefillParams &p, uint32_t g, const SeqM
 // workgroup per (partition, KV head) runs the online softmax over its keys
 // and leaves a (max, sum, o[D]) record per query vector, which
 // attn_verify_combine_kernel merges (math.rs:133-152 split over the keys).
+// A workgroup holds at most 64 query vectors (two consumer waves of 32):
+// with more (e.g. 1 + 8 drafts at G = 8), the rows are cut into slices of
+// floor(64 / G) rows, one workgroup per (partition, KV head, slice); the
+// slices of a partition are dispatched to one XCD at about the same time,
+// so the second reads the partition's pages largely from its L2 and the
+// Infinity Cache.  Each (row, head) record is written by one slice.
 // ---------------------------------------------------------------------------
 struct VerifyParams {
     PrefillParams p;       // meta[s].nblk = records per (row, head) of sequence s
     float *partials;       // records of kRecordStride floats
     uint32_t part_keys;
-    uint32_t rows_g;       // query vectors per KV head of the widest sequence (<= 64)
+    uint32_t units;           // (partition, KV head) pairs of the launch
+    uint32_t slices;          // row slices per unit (each <= 64 query vectors)
+    uint32_t rows_per_slice;  // floor(64 / G)
     uint32_t blk0[kMetaPerLaunch];  // first partition of each sequence (prefix)
     uint32_t rec0[kMetaPerLaunch];  // first record of each sequence
 };
@@ -1547,17 +1661,20 @@ constexpr int kRecordStride = D + 4;  // m, l, 2 unused, o[D] (16-byte aligned)
 // that a partition never spans more pages)
 constexpr uint32_t kVerifyPageSlots = 2048;
 
-// Tile staging of the verify producers (128 lanes, lane gt): fp16 K rows with
-// k_swz; V as fp16 rows with v_swz (kRowV: D = 128, read back with
-// transposing LDS loads, so staging V costs no more than staging K) or as V^T
+// Tile staging of the verify producers (NL lanes per tile, lane gt: 128 at
+// D <= 128, where a step stages two tiles, 256 at D = 256, one tile per
+// step): fp16 K rows with k_swz; V as fp16 rows with v_swz (kRowV: D = 128
+// and 256, read back with transposing LDS loads, so V shares K's page ids
+// and row addresses and staging it costs no more than staging K) or as V^T
 // with vt_swz (D = 64).  Every offset is recomputed from gt at each use, so
 // that only the tiles in flight occupy registers.  Page ids come from the
 // partition's LDS copy.
 template <int D>
 struct VerifyIo {
-    static constexpr bool kRowV = D == 128;
+    static constexpr bool kRowV = D >= 128;
+    static constexpr int NL = D <= 128 ? 128 : 256;         // lanes staging one tile
     static constexpr int KCH = D / 8;                       // 16-byte chunks per row
-    static constexpr int KSTEP = 128 / KCH;                 // keys per pass of the lanes
+    static constexpr int KSTEP = NL / KCH;                  // keys per pass of the lanes
     static constexpr int KL = kKeyTile / KSTEP;             // K chunks per lane
     static constexpr int VL = kKeyTile / 4 / KSTEP;         // 4-key V units per lane
     const unsigned char *k_head;  // page 0 of this KV head in the K pool
@@ -1655,35 +1772,65 @@ struct VerifyIo {
     }
 };
 
-// One workgroup of 8 waves per (partition, KV head), one workgroup per CU.
-// Waves 4..7 stream the partition's K/V tiles, two per step (lanes 0..127 of
-// the four the even tile, lanes 128..255 the odd one): kVerifyDepth steps
-// are in flight in their registers while they convert the oldest into one
-// of two LDS buffer pairs.  Waves 0..3 are two consumer pairs, one wave per
-// SIMD: pair 0 takes the even tiles, pair 1 the odd ones, each wave of a
-// pair 32 of the query vectors.  One barrier per step: after barrier k, the
-// tiles of step k are in LDS and the buffers of step k-1 are free.  Each
-// pair leaves its own record, so a partition has two.
-constexpr int kVerifyDepth = 3;
-constexpr int kVerifyThreads = 512;
-
+// One workgroup of 8 waves per (partition, KV head, row slice), one
+// workgroup per CU.  Waves 4..7 stream the partition's K/V tiles:
+// kVerifyDepth steps are in flight in their registers while they convert
+// the oldest into one of two LDS buffer sets.  Waves 0..3 consume, one wave
+// per SIMD:
+//   D <= 128: two tiles per step (lanes 0..127 of the producers stage the
+//     even tile, 128..255 the odd one); consumer pair 0 takes the even
+//     tiles, pair 1 the odd ones, each wave of a pair 32 of the query
+//     vectors.  Each pair leaves its own record, so a partition has two.
+//   D = 256: one tile per step (all 256 producer lanes); consumer wave
+//     (half, group) takes 32 query vectors and half of the output dims: the
+//     two waves of a vector group compute the same scores and softmax (the
+//     same operations on the same tile), each its 128 dims of P V.  One
+//     record per partition.
+// One barrier per step: after barrier k, the tiles of step k are in LDS and
+// the buffers of step k-1 are free.
+// steps in flight in the producers' registers: 3 at D <= 128 (measured 2-3 %
+// faster than 2, 4 slower); 2 at D = 256, whose steps hold twice the bytes
 template <int D>
+constexpr int kVerifyDepth = D <= 128 ? 3 : 2;
+constexpr int kVerifyThreads = 512;
+template <int D>
+constexpr uint32_t kVerifyTilesPerStep = D <= 128 ? 2 : 1;
+template <int D>
+constexpr size_t kVerifyTileLds = 2 * kVerifyTilesPerStep<D> * 2 * kTileBytes<D>;
+
+// kAllTiles (D <= 128 only): each of the four consumer waves takes 32 query
+// vectors and both tiles of every step (up to 128 vectors per workgroup, one
+// record per partition), for calls with more than 64 vectors per KV head.
+template <int D, bool kAllTiles>
 __global__ __launch_bounds__(kVerifyThreads) __attribute__((amdgpu_waves_per_eu(2))) void
 attn_verify_kernel(const VerifyParams vp) {
+    static_assert(!kAllTiles || D <= 128, "D = 256 splits the output dims instead");
     constexpr int NS = D / 16;
-    constexpr int NT = D / 32;
+    constexpr uint32_t TPS = kVerifyTilesPerStep<D>;
+    // records per partition (one per consumer that saw part of its tiles)
+    constexpr uint32_t kRecPerPart = kAllTiles ? 1 : TPS;
+    constexpr int NTW = D <= 128 ? D / 32 : 4;  // output tiles of a consumer wave
     extern __shared__ __align__(16) unsigned char lds[];
     const PrefillParams &p = vp.p;
 
     const int tid = threadIdx.x;
     const int wave = wave_index();
     const int lane = tid & 63;
-    const uint32_t kvh = blockIdx.x % p.kv_heads;
-    const uint32_t j = blockIdx.x / p.kv_heads;
+    // block -> (unit, slice): the slices of a unit are 8 blocks apart, so
+    // they land on the same XCD (block i runs on XCD i % 8) at about the
+    // same time; blocks past the last unit leave at once (whole workgroup)
+    const uint32_t grp8 = blockIdx.x / (8 * vp.slices);
+    const uint32_t slice = (blockIdx.x / 8) % vp.slices;
+    const uint32_t unit = grp8 * 8 + blockIdx.x % 8;
+    if (unit >= vp.units) return;
+    const uint32_t kvh = unit % p.kv_heads;
+    const uint32_t j = unit / p.kv_heads;
     uint32_t s = 0;
     while (s + 1 < p.nseq && vp.blk0[s + 1] <= j) ++s;
-    const QArgs qa = q_args(p);
     const PrefillMeta m = p.meta[s];
+    const uint32_t row_begin = slice * vp.rows_per_slice;
+    if (row_begin >= m.rows) return;  // this sequence has fewer slices (whole workgroup)
+    const QArgs qa = q_args(p);
     const uint32_t part = j - vp.blk0[s];
     const uint32_t total = m.ctx + m.rows;
     const uint32_t key_begin = part * vp.part_keys;
@@ -1691,18 +1838,18 @@ attn_verify_kernel(const VerifyParams vp) {
     const uint32_t t0 = key_begin / kKeyTile;
     const uint32_t t1 = (key_end + kKeyTile - 1) / kKeyTile;
     // both roles run the same padded number of steps (one barrier each)
-    const uint32_t steps = (t1 - t0 + 1) / 2;
-    const uint32_t k_pad = (steps + kVerifyDepth - 1) / kVerifyDepth * kVerifyDepth;
-    // buffer (step parity b, pair q): K tile, then V^T tile
+    const uint32_t steps = (t1 - t0 + TPS - 1) / TPS;
+    const uint32_t k_pad = (steps + kVerifyDepth<D> - 1) / kVerifyDepth<D> * kVerifyDepth<D>;
+    // buffer (step parity b, tile q of the step): K tile, then V tile
     auto tile_lds = [&](uint32_t k, uint32_t q) {
-        return lds + ((k & 1) * 2 + q) * 2 * kTileBytes<D>;
+        return lds + ((k & 1) * TPS + q) * 2 * kTileBytes<D>;
     };
 
     if (wave >= 4) {
         // ---- producers ----
-        const uint32_t pt = tid - 256;  // 0..255
-        const uint32_t q = pt >> 7;     // which tile of the step
-        const uint32_t gt0 = pt & 127;
+        const uint32_t pt = tid - 256;                 // 0..255
+        const uint32_t q = TPS == 2 ? pt >> 7 : 0u;    // which tile of the step
+        const uint32_t gt0 = TPS == 2 ? pt & 127 : pt;
         VerifyIo<D> io;
         io.lpt = p.log2_page_tokens;
         io.pt_mask = (1u << io.lpt) - 1;
@@ -1713,7 +1860,7 @@ attn_verify_kernel(const VerifyParams vp) {
         io.last_tok = total - 1;
         // the page ids of the partition's keys go to LDS once, so that no
         // tile load waits on a page-table read
-        int32_t *pids = (int32_t *)(lds + 8 * kTileBytes<D>);
+        int32_t *pids = (int32_t *)(lds + kVerifyTileLds<D>);
         const int32_t *table = p.page_table + (size_t)m.slot * p.pages_per_seq;
         io.first = key_begin >> io.lpt;
         const uint32_t n = ((key_end - 1) >> io.lpt) - io.first + 1;
@@ -1732,16 +1879,16 @@ attn_verify_kernel(const VerifyParams vp) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_barrier();  // (A) the producers share pids
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        u32x4 kreg[kVerifyDepth][VerifyIo<D>::KL];
-        u32x4 vreg[kVerifyDepth][4 * VerifyIo<D>::VL];
+        u32x4 kreg[kVerifyDepth<D>][VerifyIo<D>::KL];
+        u32x4 vreg[kVerifyDepth<D>][4 * VerifyIo<D>::VL];
 #pragma unroll
-        for (int u = 0; u < kVerifyDepth; ++u) {
-            io.load(kreg[u], vreg[u], min(t0 + 2 * u + q, t1 - 1), gt0);
+        for (int u = 0; u < kVerifyDepth<D>; ++u) {
+            io.load(kreg[u], vreg[u], min(t0 + TPS * u + q, t1 - 1), gt0);
             __builtin_amdgcn_sched_barrier(0);
         }
-        for (uint32_t kb = 0; kb < k_pad; kb += kVerifyDepth) {
+        for (uint32_t kb = 0; kb < k_pad; kb += kVerifyDepth<D>) {
 #pragma unroll
-            for (int u = 0; u < kVerifyDepth; ++u) {
+            for (int u = 0; u < kVerifyDepth<D>; ++u) {
                 // offsets are recomputed from a fresh copy of the lane id
                 // each step instead of being held live across the loop
                 uint32_t gt = gt0;
@@ -1751,7 +1898,7 @@ attn_verify_kernel(const VerifyParams vp) {
                 // tiles past t1 store a repeat of the last tile nobody reads
                 io.store(kreg[u], vreg[u], kt, kt + kTileBytes<D>, gt);
                 __syncthreads();  // (B) the tiles of step k are in LDS
-                io.load(kreg[u], vreg[u], min(t0 + 2 * (k + kVerifyDepth) + q, t1 - 1), gt);
+                io.load(kreg[u], vreg[u], min(t0 + TPS * (k + kVerifyDepth<D>) + q, t1 - 1), gt);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -1759,15 +1906,17 @@ attn_verify_kernel(const VerifyParams vp) {
     }
 
     // ---- consumers ----
-    const uint32_t pair = wave >> 1;
-    const int cw = wave & 1;  // which 32 query vectors
+    // tile of the step (pair mode), output dims (D = 256), 32-vector group
+    const uint32_t pair = (TPS == 2 && !kAllTiles) ? (uint32_t)wave >> 1 : 0u;
+    const uint32_t half = TPS == 2 ? 0u : (uint32_t)wave >> 1;
+    const int cw = kAllTiles ? wave : (wave & 1);
     const int h = lane >> 5;
     const int col = lane & 31;
     const uint32_t G = p.heads / p.kv_heads;
-    const uint32_t nvec = m.rows * G;
+    const uint32_t nvec = min(vp.rows_per_slice, m.rows - row_begin) * G;
     const bool computes = 32u * cw < nvec;               // wave-uniform
     const uint32_t vec = min(32u * cw + col, nvec - 1);  // this lane's query vector
-    const uint32_t r = vec / G;
+    const uint32_t r = row_begin + vec / G;
     const uint32_t head = kvh * G + vec % G;
     const uint32_t key_limit = m.ctx + r;
     const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
@@ -1778,18 +1927,16 @@ attn_verify_kernel(const VerifyParams vp) {
     __builtin_amdgcn_s_barrier();  // (A)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 
-    f32x16 oacc[NT];
+    f32x16 oacc[NTW];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
-    uint32_t voff[NT];
-    if constexpr (VerifyIo<D>::kRowV) pv_rows_offsets<D>(lane, voff);
+    for (int t = 0; t < NTW; ++t) oacc[t] = f32x16{};
+    uint32_t voff[NTW];
+    if constexpr (VerifyIo<D>::kRowV) pv_rows_offsets<D, NTW>(lane, voff, NTW * half);
     float m_run = -INFINITY;
     float l_run = 0.0f;
-    for (uint32_t k = 0; k < k_pad; ++k) {
-        __syncthreads();  // (B)
-        const uint32_t t = t0 + 2 * k + pair;
-        if (!computes || t >= t1) continue;
-        const unsigned char *kt = tile_lds(k, pair);
+    // one tile of step k: scores, softmax, P V
+    auto consume = [&](uint32_t k, uint32_t tq, uint32_t t) __attribute__((always_inline)) {
+        const unsigned char *kt = tile_lds(k, tq);
         const unsigned char *vt = kt + kTileBytes<D>;
         const uint32_t key0 = t * kKeyTile;
         f32x16 sacc[2];
@@ -1807,26 +1954,41 @@ attn_verify_kernel(const VerifyParams vp) {
                 }
         }
         f16x8 pop[4];
-        softmax_tile<D>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
-        if constexpr (VerifyIo<D>::kRowV) pv_tile_rows<D>(vt, voff, pop, oacc);
+        // (the softmax's D only sizes the O tiles it rescales: NTW of them)
+        softmax_tile<32 * NTW>(sacc, key0, edge, key_limit, h, m_run, l_run, oacc, pop);
+        if constexpr (VerifyIo<D>::kRowV) pv_tile_rows<D, NTW>(vt, voff, pop, oacc);
         else pv_tile<D>(vt, pop, h, col, oacc);
+    };
+    for (uint32_t k = 0; k < k_pad; ++k) {
+        __syncthreads();  // (B)
+        if constexpr (kAllTiles) {
+            const uint32_t t = t0 + TPS * k;
+            if (!computes || t >= t1) continue;
+            consume(k, 0, t);
+            if (t + 1 >= t1) continue;
+            consume(k, 1, t + 1);
+        } else {
+            const uint32_t t = t0 + TPS * k + pair;
+            if (!computes || t >= t1) continue;
+            consume(k, pair, t);
+        }
     }
     const float l = xhalf_sum(l_run);
     if (32u * cw + col >= nvec) return;
     // record (sequence s, row r, head, partition, pair): o unnormalised
-    const uint32_t nrec = m.nblk;  // records per (row, head): two per partition
-    float *rec = vp.partials +
-                 ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nrec + 2 * part + pair) *
-                     kRecordStride<D>;
-    if (h == 0) {
+    const uint32_t nrec = m.nblk;  // records per (row, head): kRecPerPart per partition
+    float *rec = vp.partials + ((size_t)vp.rec0[s] + ((size_t)r * p.heads + head) * nrec +
+                                kRecPerPart * part + pair) *
+                                   kRecordStride<D>;
+    if (h == 0 && half == 0) {
         // a pair that saw no key of this row's range has l = 0
         *(float2 *)rec = make_float2(l > 0.0f ? m_run : -INFINITY, l);
     }
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt)
+    for (int tt = 0; tt < NTW; ++tt)
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
-            const uint32_t d0 = 32 * tt + 8 * a + 4 * h;
+            const uint32_t d0 = 128 * half + 32 * tt + 8 * a + 4 * h;
             *(float4 *)(rec + 4 + d0) = make_float4(oacc[tt][4 * a], oacc[tt][4 * a + 1],
                                                     oacc[tt][4 * a + 2], oacc[tt][4 * a + 3]);
         }
@@ -1927,15 +2089,18 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_verify_combine_kernel
     if (!finite) atomicOr(p.err_word, kErrPrefillRange);
 }
 
-template <int D>
+template <int D, bool kAllTiles>
 hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
                            uint32_t combine_rows) {
-    const size_t lds = 8 * kTileBytes<D> + kVerifyPageSlots * sizeof(int32_t);
-    static const hipError_t configured = hipFuncSetAttribute(
-        (const void *)attn_verify_kernel<D>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    const size_t lds = kVerifyTileLds<D> + kVerifyPageSlots * sizeof(int32_t);
+    static_assert(kVerifyTileLds<D> + kVerifyPageSlots * sizeof(int32_t) <= 160 * 1024,
+                  "verify LDS");
+    static const hipError_t configured =
+        hipFuncSetAttribute((const void *)attn_verify_kernel<D, kAllTiles>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (configured != hipSuccess) return configured;
-    SR_LAUNCH("attn_verify_kernel", attn_verify_kernel<D>, dim3(blocks), dim3(kVerifyThreads), lds,
-              stream, vp);
+    SR_LAUNCH("attn_verify_kernel", (attn_verify_kernel<D, kAllTiles>), dim3(blocks),
+              dim3(kVerifyThreads), lds, stream, vp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     SR_LAUNCH("attn_verify_combine_kernel", attn_verify_combine_kernel<D>, dim3(combine_rows),
@@ -2011,8 +2176,9 @@ hipError_t launch_attn_prefill(hipStream_t stream, const AttnLaunch &a, const Se
 }
 
 bool verify_supported(const AttnLaunch &a, uint32_t rows) {
-    return prefill_supported(a) && a.head_dim <= 128 && rows >= 2 &&
-           rows * (a.heads / (a.kv_heads * a.kv_rep)) <= 64;
+    // any rows (the router sends 2..15): more than 64 query vectors per KV
+    // head run as row slices
+    return prefill_supported(a) && rows >= 2;
 }
 
 hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const SeqMeta *seqs,
@@ -2026,21 +2192,26 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
     // partition size: one workgroup per CU over the whole call, at least
     // 256 keys, a multiple of the 64-key tile
     uint64_t keys = 0;
-    uint32_t max_rows = 0, rows_g = 0;
+    uint32_t max_rows = 0;
     for (int i = 0; i < nseq; ++i) {
         if (!verify_supported(a, seqs[i].rows)) return hipErrorInvalidValue;
         keys += (uint64_t)seqs[i].ctx + seqs[i].rows;
         max_rows = std::max(max_rows, seqs[i].rows);
-        rows_g = std::max(rows_g, seqs[i].rows * g);
     }
+    // query vectors per workgroup: 64 in the pair mode; at D <= 128 a call
+    // with more runs every consumer wave over both tiles of a step (128);
+    // rows beyond run as further slices of the rows
+    const bool all_tiles = a.head_dim <= 128 && max_rows * g > 64;
+    vp.rows_per_slice = (all_tiles ? 128 : 64) / g;
+    vp.slices = (max_rows + vp.rows_per_slice - 1) / vp.rows_per_slice;
     const uint64_t target = (uint64_t)std::max(in.num_cus, 1);
-    uint64_t part = (keys * kvv + target - 1) / target;
+    uint64_t part = (keys * kvv * vp.slices + target - 1) / target;
     part = std::max<uint64_t>(256, (part + kKeyTile - 1) / kKeyTile * kKeyTile);
     // a partition starting mid-page touches at most part/page_tokens + 2 pages
     const uint64_t max_part =
         ((uint64_t)(kVerifyPageSlots - 2) * a.pool->page_tokens) / kKeyTile * kKeyTile;
     vp.part_keys = (uint32_t)std::min<uint64_t>(std::min(part, max_part), 1u << 30);
-    vp.rows_g = rows_g;
+    const uint32_t tps = (a.head_dim <= 128 && !all_tiles) ? 2 : 1;  // records per partition
     uint32_t blocks = 0, records = 0, waves = 0;
     for (int i = 0; i < nseq; ++i) {
         PrefillMeta &m = p.meta[i];
@@ -2049,7 +2220,7 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         m.rows = seqs[i].rows;
         m.row0 = seqs[i].row0;
         const uint32_t parts = (m.ctx + m.rows + vp.part_keys - 1) / vp.part_keys;
-        m.nblk = 2 * parts;  // records per (row, head): one per consumer pair
+        m.nblk = tps * parts;  // records per (row, head): one per tile of a step
         vp.blk0[i] = blocks;
         vp.rec0[i] = records;
         blocks += parts;
@@ -2057,17 +2228,29 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         waves += m.rows * a.heads;
     }
     p.max_blk = 0;
-    const size_t stride = (a.head_dim == 64 ? kRecordStride<64> : kRecordStride<128>);
+    const size_t stride = a.head_dim == 64    ? kRecordStride<64>
+                          : a.head_dim == 128 ? kRecordStride<128>
+                                              : kRecordStride<256>;
     vp.partials = in.reserve_partials((size_t)records * stride * sizeof(float));
     if (vp.partials == nullptr) return hipErrorOutOfMemory;
     // K/V of the new rows and their RoPE cos/sin first (append kernel)
     if (a.head_dim == 64) launch_append<64>(stream, p, max_rows);
-    else launch_append<128>(stream, p, max_rows);
+    else if (a.head_dim == 128) launch_append<128>(stream, p, max_rows);
+    else launch_append<256>(stream, p, max_rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t grid = blocks * kvv;
-    if (a.head_dim == 64) return launch_verify_d<64>(stream, vp, grid, waves);
-    return launch_verify_d<128>(stream, vp, grid, waves);
+    vp.units = blocks * kvv;
+    // (unit, slice) blocks: groups of 8 units, each group's slices 8 apart
+    const uint32_t grid = (vp.units + 7) / 8 * 8 * vp.slices;
+    if (a.head_dim == 64) {
+        return all_tiles ? launch_verify_d<64, true>(stream, vp, grid, waves)
+                         : launch_verify_d<64, false>(stream, vp, grid, waves);
+    }
+    if (a.head_dim == 128) {
+        return all_tiles ? launch_verify_d<128, true>(stream, vp, grid, waves)
+                         : launch_verify_d<128, false>(stream, vp, grid, waves);
+    }
+    return launch_verify_d<256, false>(stream, vp, grid, waves);
 }
 
 }  // namespace sr

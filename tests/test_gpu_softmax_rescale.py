@@ -250,13 +250,16 @@ def test_lockstep_prefill_rising_thresholds_and_falls(pkg, backend, rng, heads, 
 # MTP verify (2..15 rows): split-K partitions, each with its own maximum
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("heads,kv_heads,rows", [(64, 8, 5), (32, 8, 3), (40, 8, 9)])
-def test_verify_sinks_in_later_partitions(pkg, backend, rng, heads, kv_heads, rows):
+@pytest.mark.parametrize("heads,kv_heads,rows,dim", [(64, 8, 5, 128), (32, 8, 3, 128),
+                                                     (40, 8, 9, 128), (64, 8, 9, 128),
+                                                     (16, 2, 5, 256), (16, 2, 9, 256)])
+def test_verify_sinks_in_later_partitions(pkg, backend, rng, heads, kv_heads, rows, dim):
     # partitions are at least 256 keys, so a 6000-token context is cut into
     # many; every (row, head) gets a planted key at +10, +20 or +40 log2
     # units somewhere in the context, most of them past the first partition,
-    # and a second sequence has first-tile plants above every later key
-    dim = 128
+    # and a second sequence has first-tile plants above every later key.
+    # 64 / 8 with 9 rows runs as two row slices; head_dim 256 splits each
+    # workgroup's output dims over two waves that share the softmax
     pool = new_pool(pkg, backend, kv_heads, dim, page_tokens=16, max_tokens=8192, seqs=2)
     gq, gk = gammas(rng, dim)
     ctx = 6000
