@@ -182,10 +182,12 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_read(
  * Output:  out [rows][heads*head_dim] f32.
  * seq_ids and seq_rows are always host arrays.  The kernel is chosen per
  * sequence: one row goes to the split-K decode kernel; 2..15 rows (MTP
- * verify drafts) with rows * heads/kv_heads <= 64 and head_dim <= 128 to the
- * multi-row split-K verify kernel (every cached K/V tile read once for all
- * rows); 16 or more rows to the MFMA prefill kernels; anything else row by
- * row on the decode kernel.  A synchronous call whose verify or prefill rows
+ * verify drafts) to the multi-row split-K verify kernel (every cached K/V
+ * tile read once for up to 128 query vectors, rows * heads/kv_heads, at
+ * head_dim <= 128 and 64 at head_dim 256; more rows run as row slices, each
+ * reading the cache once); 16 or more rows to the MFMA prefill kernels.
+ * Query-head groups other than 1..8 heads per KV head and RoPE widths not a
+ * multiple of 32 go row by row to the decode kernel.  A synchronous call whose verify or prefill rows
  * meet a K/V/q value beyond the fp16 range of the MFMA operands
  * (|x| >= 65520) recomputes those sequences on the f32 split-K path; an
  * asynchronous one reports it at the next synchronous call.
