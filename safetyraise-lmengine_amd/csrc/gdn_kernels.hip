@@ -596,10 +596,8 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 }
 
 // ---------------------------------------------------------------------------
-// Chunked prefill: the delta rule of prefill-sized calls in chunked form,
-// the chunk-wide products on f32 MFMA (v_mfma_f32_16x16x4f32) and the state
-// products on split bf16 operands (v_mfma_f32_16x16x32_bf16, see Parts
-// below).  With k^, q^ the L2-normalised conv
+// Chunked prefill: the delta rule of prefill-sized calls in chunked form on
+// f32 MFMA (v_mfma_f32_16x16x4f32).  With k^, q^ the L2-normalised conv
 // outputs, g_t = sum_{i<=t} log(alpha_i) over the chunk and S0 the state at
 // the chunk start, the token-serial recurrence (math.rs:222-236)
 //     S_t = alpha_t S_{t-1} + delta_t k^_t^T,
@@ -623,8 +621,7 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 //       Pm[t][j] = e^{g_t-g_j} (q^_t . k^_j) (j <= t),  e^{g_C}
 //     and, from the last chunk, the next conv history;
 //   gdn_chunk_scan_kernel: one workgroup per (sequence, value head, 32 of the
-//     Dv = 128 state rows), the f32 slice in the registers of the waves that
-//     update it and its bf16 parts in LDS, walking the chunks in order:
+//     Dv = 128 state rows), the slice in LDS, walking the chunks in order:
 //       Delta = U + (-W) S0^T,  o = (Qe S0^T + Pm Delta) / sqrt(Dk),
 //       S_C = e^{g_C} S0 + Delta^T Ks^T.
 // The conv history is double-buffered exactly as in gdn_delta_kernel.
@@ -667,10 +664,7 @@ __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(1.4426950408889634f * x);
 }
 
-// One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.  Qe,
-// -W, Ks and Pm are the scan's MFMA operands and are stored as their two
-// bf16 parts (the hi plane, then the lo plane, in the matrix's own floats);
-// U and e^{g_C} stay f32.
+// One (chunk, value head) record of gdn_chunk_prep_kernel, in floats.
 constexpr int kRecQe = 0;                      // [kCk][kDk]     Qe
 constexpr int kRecWn = kRecQe + kCk * kDk;     // [kCk][kDk]     -W
 constexpr int kRecU = kRecWn + kCk * kDk;      // [kCk][kHeadDv] U
@@ -680,66 +674,17 @@ constexpr int kRecEc = kRecPm + kCk * kCk;     // e^{g_C}
 constexpr int kRecFloats = kRecEc + 64;        // a 256-byte multiple
 constexpr int kPre = kMaxK - 1;                // raw input rows staged before a chunk
 
-// The scan's products run on bf16 MFMA with each f32 operand split in two
-// parts, hi = bf16(x) and lo = bf16(x - hi) (round to nearest even; x - hi
-// is exact), and a product taken as hi.hi + hi.lo + lo.hi: every part
-// product is exact in f32, and what is left out (lo.lo and the remainder
-// x - hi - lo) is below 2^-15 of the product.  A matrix lives in LDS as its
-// two part planes, rows padded against bank conflicts.
-constexpr int kPh = kDk + 8;  // pitch (bf16) of [.][Dk] planes
-constexpr int kPq = kCk + 8;  // pitch (bf16) of [.][chunk] planes
-
-template <int R, int P>
-struct Parts {
-    uint16_t hi[R][P];
-    uint16_t lo[R][P];
-};
-
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-// bf16's largest finite value (0x7F7F).  The hi part of a split is taken
-// from x clamped to it, so a finite x above it still splits into finite
-// parts (x - hi exact); an infinite x leaves a NaN part, and the row's output
-// is non-finite as the reference's would be.
-constexpr float kBf16Max = 3.38953139e38f;
-
-__device__ __forceinline__ float bf16_range(float x) {
-    return __builtin_amdgcn_fmed3f(x, -kBf16Max, kBf16Max);
-}
-__device__ __forceinline__ f32x4 bf16_range(const f32x4 &x) {
-    return f32x4{bf16_range(x.x), bf16_range(x.y), bf16_range(x.z), bf16_range(x.w)};
-}
-
-// Element i (or four from i) of an n-element record matrix at float offset
-// `off`, written as its parts: hi plane at element i, lo plane at n + i.
-__device__ __forceinline__ void rec_put1(float *rec, int off, int n, int i, float x) {
-    uint16_t *m = (uint16_t *)(rec + off);
-    const __bf16 hi = (__bf16)bf16_range(x);
-    const __bf16 lo = (__bf16)(x - (float)hi);
-    m[i] = __builtin_bit_cast(uint16_t, hi);
-    m[n + i] = __builtin_bit_cast(uint16_t, lo);
-}
-__device__ __forceinline__ void rec_put4(float *rec, int off, int n, int i, const f32x4 &x) {
-    uint16_t *m = (uint16_t *)(rec + off);
-    const bf16x4 hi = __builtin_convertvector(bf16_range(x), bf16x4);
-    const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
-    *(bf16x4 *)(m + i) = hi;
-    *(bf16x4 *)(m + n + i) = lo;
-}
-
 struct ScanLds {
-    Parts<kVs, kPh> s0;  // state slice parts: rows v, dims d
-    Parts<kVs, kPq> dt;  // Delta of the slice, transposed: [v][t]
-    struct Rec {         // a chunk's record
-        Parts<kCk, kPh> qe;
-        Parts<kCk, kPh> wn;
-        Parts<kDk, kPq> ks;
-        Parts<kCk, kPq> pm;
-        float u[kCk][kPc];  // this slice's columns of U, f32 (the Delta accumulators' start)
+    float s0[kVs][kPr];  // state slice: rows v, dims d
+    float dt[kVs][kPc];  // Delta of the slice, transposed: [v][t]
+    struct Rec {         // a chunk's record, rows padded against bank conflicts
+        float qe[kCk][kPr];
+        float wn[kCk][kPr];
+        float ks[kDk][kPc];
+        float pm[kCk][kPc];
+        float u[kCk][kPc];  // this slice's columns of U
     } r[2];
 };
-static_assert(sizeof(ScanLds) <= 160 * 1024, "scan LDS");
 
 __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -782,52 +727,6 @@ __device__ __forceinline__ void mma(f32x4 &acc, const Ops<NK> &a, const Ops<NK> 
         acc = mfma4(a.v[s].z, b.v[s].z, acc);
         acc = mfma4(a.v[s].w, b.v[s].w, acc);
     }
-}
-
-// Four consecutive elements of row `row` from column `col` into the planes.
-template <int R, int P>
-__device__ __forceinline__ void put_parts(Parts<R, P> &m, int row, int col, const f32x4 &x) {
-    const bf16x4 hi = __builtin_convertvector(bf16_range(x), bf16x4);
-    const bf16x4 lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
-    *(bf16x4 *)&m.hi[row][col] = hi;
-    *(bf16x4 *)&m.lo[row][col] = lo;
-}
-
-// One lane's parts of a 16-row tile over NS steps of 32 k: row lane & 15,
-// k = 32 s + 8 (lane >> 4) + j, the v_mfma_f32_16x16x32_bf16 operand layout
-// (A row r and B row r at the same k; the tile's rows 4 slot + i, column r
-// are acc[i], as for the f32 form).
-template <int NS>
-struct Ops2 {
-    bf16x8 hi[NS], lo[NS];
-};
-
-template <int NS, int R, int P>
-__device__ __forceinline__ void load_ops2(Ops2<NS> &o, const Parts<R, P> &m, int row0, int lane) {
-    const int r = row0 + (lane & 15), c = 8 * (lane >> 4);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        o.hi[s] = *(const bf16x8 *)&m.hi[r][32 * s + c];
-        o.lo[s] = *(const bf16x8 *)&m.lo[r][32 * s + c];
-    }
-}
-
-__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// acc + A B^T: the hi.hi products accumulate onto acc, the two cross terms in
-// a second chain that is added at the end.
-template <int NS>
-__device__ __forceinline__ f32x4 mma2(f32x4 acc, const Ops2<NS> &a, const Ops2<NS> &b) {
-    f32x4 x = {0, 0, 0, 0};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        acc = mfma_bf16(a.hi[s], b.hi[s], acc);
-        x = mfma_bf16(a.hi[s], b.lo[s], x);
-        x = mfma_bf16(a.lo[s], b.hi[s], x);
-    }
-    return acc + x;
 }
 
 // Causal conv channel with the kernel size K known at compile time; same
@@ -1166,8 +1065,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
         for (int e = first; e < kDk * kCk / 4; e += stride) {
             const int d = e >> 3, j = 4 * (e & 7);
-            rec_put4(rec, kRecKs, kDk * kCk, d * kCk + j,
-                     *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j]);
+            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
+                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
         }
     };
     if (wave < 3 || kW) {
@@ -1199,8 +1098,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             if (wave < 3) {
                 L.a[t][j] = j < t ? L.beta[t] * e * L.rk[t] * rkj * acc[i] : 0.0f;
             } else {
-                rec_put1(rec, kRecPm, kCk * kCk, t * kCk + j, e * L.rq[t] * rkj * acc[i]);
-                rec_put1(rec, kRecPm, kCk * kCk, t * kCk + 16 + r16, 0.0f);
+                rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
+                rec[kRecPm + t * kCk + 16 + r16] = 0.0f;
             }
         }
     } else if (kW) {
@@ -1211,7 +1110,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             // Qe = diag(e^{g_t} / |q_t|) Q
             const int e = u + n * 256;
             const int t = e >> 5, d = 4 * (e & 31);
-            rec_put4(rec, kRecQe, kCk * kDk, t * kDk + d, *(const f32x4 *)&L.qv.q[t][d] * L.qs[t]);
+            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.qv.q[t][d] * L.qs[t];
         }
         if (kU) write_ks(u, 256);
     } else {
@@ -1261,7 +1160,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * p1_tr + 4 * sl + i;
             const float e = j <= t ? fast_exp(L.g[t] - gj) : 0.0f;
-            rec_put1(rec, kRecPm, kCk * kCk, t * kCk + j, e * L.rq[t] * rkj * acc[i]);
+            rec[kRecPm + t * kCk + j] = e * L.rq[t] * rkj * acc[i];
         }
     }
     __syncthreads();
@@ -1289,8 +1188,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
     //      32 (w >> 1) .. + 31
     {
         const int tr = wave & 1, c0 = 32 * (wave >> 1);
-        // -W goes to the record as its parts, U as f32
-        auto product = [&](const float *scale, const float (*rows)[kPc], int off, bool parts)
+        auto product = [&](const float *scale, const float (*rows)[kPc], float *dst, float sign)
                            __attribute__((always_inline)) {
             Ops<2> ta;
             load_ops(ta, &L.t[16 * tr][0], kPc, lane);
@@ -1310,12 +1208,11 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
-                    if (parts) rec_put1(rec, off, kCk * kDk, t * kDk + col, -o[n][i]);
-                    else rec[off + t * kDk + col] = o[n][i];
+                    dst[t * kDk + col] = sign * o[n][i];
                 }
         };
-        if (kW) product(L.sw, L.kc, kRecWn, true);
-        if (kU) product(L.su, L.qv.vc, kRecU, false);
+        if (kW) product(L.sw, L.kc, rec + kRecWn, -1.0f);
+        if (kU) product(L.su, L.qv.vc, rec + kRecU, 1.0f);
     }
 }
 
@@ -1323,10 +1220,9 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
 // state, 8 waves: waves 0..3 own the output tiles (rows 16 (w >> 1)..,
 // state rows 16 (w & 1)..), waves 4..7 the Delta tiles of the same places
 // and then the state-update tiles (state rows 16 ((w - 4) >> 1)..,
-// dims 64 ((w - 4) & 1)..), so each SIMD runs one wave of each kind; the
-// latter hold the slice's f32 state in registers between chunks.  Each
-// chunk's record (the parts of Qe, -W, Pm and Ks, and this slice's f32 U
-// columns) is copied once per workgroup into LDS,
+// dims 64 ((w - 4) & 1)..), so each SIMD runs one wave of each kind and the
+// same MFMA count in both phases.  Each chunk's record (Qe, -W, Pm, Ks and
+// this slice's U columns) is staged once per workgroup into LDS,
 // double-buffered: the loads for chunk c + 1 are issued into registers at
 // the start of chunk c and written to the other buffer at its end, so they
 // have a whole chunk to land.  xcd_map: the grid is ordered so that the four
@@ -1360,53 +1256,48 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
     const uint32_t nchunks = (m.rows + kCk - 1) / kCk;
     const float qscale = 1.0f / sqrtf((float)kDk);  // math.rs:234-235
 
-    // record staging: 7 16-byte segments per thread.  Qe, -W and Ks are
-    // 1024 segments each in the record, hi plane then lo plane: segment
-    // e = tid + 512 (n & 1) is in plane n & 1.  The last segment is Pm's
-    // (output waves: 256 segments, plane t2 >> 7) or this slice's U columns.
+    // record staging: 7 16-byte segments per thread; segment e = tid + 512 n
+    // is in Qe (n < 2), -W (n < 4), Ks (n < 6), then Pm (waves 0..3) or U
     constexpr int kSeg = 7;
     auto rec_of = [&](uint32_t c) -> const float * {
         return p.chunk_rec + ((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats;
     };
     const int t2 = tid & 255;
-    auto fetch = [&](const float *rec, u32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+    auto fetch = [&](const float *rec, f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
 #pragma unroll
         for (int n = 0; n < kSeg; ++n) {
             const int e = tid + kScanThreads * (n & 1);
             int src;
-            if (n < 2) src = kRecQe + 4 * e;
-            else if (n < 4) src = kRecWn + 4 * e;
-            else if (n < 6) src = kRecKs + 4 * e;
-            else if (out_wave) src = kRecPm + 4 * t2;
+            if (n < 2) src = kRecQe + (e >> 5) * kDk + 4 * (e & 31);
+            else if (n < 4) src = kRecWn + (e >> 5) * kDk + 4 * (e & 31);
+            else if (n < 6) src = kRecKs + (e >> 3) * kCk + 4 * (e & 7);
+            else if (out_wave) src = kRecPm + (t2 >> 3) * kCk + 4 * (t2 & 7);
             else src = kRecU + (t2 >> 3) * kHeadDv + vq * kVs + 4 * (t2 & 7);
-            xs[n] = *(const u32x4 *)(rec + src);
+            xs[n] = *(const f32x4 *)(rec + src);
         }
     };
-    auto put = [&](ScanLds::Rec &r, const u32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
+    auto put = [&](ScanLds::Rec &r, const f32x4 (&xs)[kSeg]) __attribute__((always_inline)) {
 #pragma unroll
         for (int n = 0; n < kSeg; ++n) {
-            uint16_t *dst;
-            if (n < 2) dst = (n & 1 ? r.qe.lo : r.qe.hi)[tid >> 4] + 8 * (tid & 15);
-            else if (n < 4) dst = (n & 1 ? r.wn.lo : r.wn.hi)[tid >> 4] + 8 * (tid & 15);
-            else if (n < 6) dst = (n & 1 ? r.ks.lo : r.ks.hi)[tid >> 2] + 8 * (tid & 3);
-            else if (out_wave) dst = (t2 >> 7 ? r.pm.lo : r.pm.hi)[(t2 & 127) >> 2] + 8 * (t2 & 3);
-            else dst = (uint16_t *)&r.u[t2 >> 3][4 * (t2 & 7)];
-            *(u32x4 *)dst = xs[n];
+            const int e = tid + kScanThreads * (n & 1);
+            float *dst;
+            if (n < 2) dst = &r.qe[e >> 5][4 * (e & 31)];
+            else if (n < 4) dst = &r.wn[e >> 5][4 * (e & 31)];
+            else if (n < 6) dst = &r.ks[e >> 3][4 * (e & 7)];
+            else if (out_wave) dst = &r.pm[t2 >> 3][4 * (t2 & 7)];
+            else dst = &r.u[t2 >> 3][4 * (t2 & 7)];
+            *(f32x4 *)dst = xs[n];
         }
     };
-    u32x4 xs[kSeg];
+    f32x4 xs[kSeg];
     fetch(rec_of(0), xs);
     float *state = p.state + (((size_t)m.state_in * p.value_heads + h) * kHeadDv + vq * kVs) * kDk;
-    // The Delta waves own the slice's f32 state in registers: wave (tr, tc)
-    // state rows 16 tr + (lane & 15), dims 64 tc + 16 n + 4 (lane >> 4) + i,
-    // the layout of their state-update tiles; LDS holds its parts
-    const int sv = 16 * tr + r16;
-    f32x4 s0r[4];
-    if (!out_wave) {
+    {
+        const int v = tid >> 4, d0 = (tid & 15) * 4;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) s0r[n] = *(const f32x4 *)(state + (size_t)sv * kDk + 64 * tc + 16 * n + 4 * sl);
-#pragma unroll
-        for (int n = 0; n < 4; ++n) put_parts(L.s0, sv, 64 * tc + 16 * n + 4 * sl, s0r[n]);
+        for (int i = 0; i < 2; ++i) {
+            *(float4 *)&L.s0[v][d0 + 64 * i] = *(const float4 *)(state + (size_t)v * kDk + d0 + 64 * i);
+        }
     }
     put(L.r[0], xs);
     if (nchunks > 1) fetch(rec_of(1), xs);
@@ -1417,24 +1308,33 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
         ScanLds::Rec &R = L.r[c & 1];
         // phase 1, tile (rows 16 tr.., state rows 16 tc..): output waves
         // Qe S0^T, Delta waves U + (-W) S0^T
-        Ops2<kDk / 32> xa, sb;
-        load_ops2(xa, out_wave ? R.qe : R.wn, 16 * tr, lane);
-        load_ops2(sb, L.s0, 16 * tc, lane);
-        f32x4 acc = {0, 0, 0, 0};
+        Ops<kDk / 16> xa, sb;
+        load_ops(xa, out_wave ? &R.qe[16 * tr][0] : &R.wn[16 * tr][0], kPr, lane);
+        load_ops(sb, &L.s0[16 * tc][0], kPr, lane);
+        f32x4 acc = {0, 0, 0, 0}, acc2 = {0, 0, 0, 0};
         if (!out_wave) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = R.u[16 * tr + 4 * sl + i][16 * tc + r16];
         }
-        acc = mma2(acc, xa, sb);
-        // Delta^T: [v = 16 tc + r16][t = 16 tr + 4 sl + i]
-        if (!out_wave) put_parts(L.dt, 16 * tc + r16, 16 * tr + 4 * sl, acc);
+#pragma unroll
+        for (int st = 0; st < kDk / 16; ++st)
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                acc = mfma4(xa.v[st][e], sb.v[st][e], acc);
+                acc2 = mfma4(xa.v[st][e + 1], sb.v[st][e + 1], acc2);
+            }
+        acc += acc2;
+        if (!out_wave) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) L.dt[16 * tc + r16][16 * tr + 4 * sl + i] = acc[i];
+        }
         __syncthreads();
         if (out_wave) {
             // o += Pm Delta
-            Ops2<1> pa, db;
-            load_ops2(pa, R.pm, 16 * tr, lane);
-            load_ops2(db, L.dt, 16 * tc, lane);
-            acc = mma2(acc, pa, db);
+            Ops<2> pa, db;
+            load_ops(pa, &R.pm[16 * tr][0], kPc, lane);
+            load_ops(db, &L.dt[16 * tc][0], kPc, lane);
+            mma(acc, pa, db);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t t = 16 * tr + 4 * sl + i;
@@ -1444,24 +1344,33 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
                 }
             }
         } else {
-            // S_C = e^{g_C} S0 + Delta^T Ks^T over state rows 16 tr.., dims
-            // 64 tc..: tile n is Ks Delta (rows: dims 64 tc + 16 n.., columns:
-            // state rows 16 tr..), the transposed layout of s0r
+            // S_C = e^{g_C} S0 + Delta^T Ks^T over state rows 16 tr.., dims 64 tc..
             const float eC = p.chunk_rec[((size_t)(m.chunk0 + c) * p.value_heads + h) * kRecFloats + kRecEc];
-            Ops2<1> da;
-            load_ops2(da, L.dt, 16 * tr, lane);
-            Ops2<1> kb4[4];
+            Ops<2> da;
+            load_ops(da, &L.dt[16 * tr][0], kPc, lane);
+            Ops<2> kb4[4];
 #pragma unroll
-            for (int n = 0; n < 4; ++n) load_ops2(kb4[n], R.ks, 64 * tc + 16 * n, lane);
+            for (int n = 0; n < 4; ++n) load_ops(kb4[n], &R.ks[64 * tc + 16 * n][0], kPc, lane);
+            float s0v[4][4];
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                const f32x4 d = mma2(f32x4{0, 0, 0, 0}, kb4[n], da);
-                s0r[n] = d + eC * s0r[n];
-            }
-            // each of these waves rewrites exactly the S0 parts of its own
-            // rows and dims; all reads of S0 ended before the barrier above
+            for (int n = 0; n < 4; ++n)
 #pragma unroll
-            for (int n = 0; n < 4; ++n) put_parts(L.s0, sv, 64 * tc + 16 * n + 4 * sl, s0r[n]);
+                for (int i = 0; i < 4; ++i) s0v[n][i] = L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16];
+            f32x4 s4[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+            for (int st = 0; st < 2; ++st)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+#pragma unroll
+                    for (int n = 0; n < 4; ++n) s4[n] = mfma4(da.v[st][e], kb4[n].v[st][e], s4[n]);
+            // each of these waves rewrites exactly the S0 elements it read
+            // into s0v; all other reads of S0 ended before the barrier above
+#pragma unroll
+            for (int n = 0; n < 4; ++n)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    L.s0[16 * tr + 4 * sl + i][64 * tc + 16 * n + r16] = s4[n][i] + eC * s0v[n][i];
+                }
         }
         // the next chunk's record into the other buffer (last read in the
         // previous chunk), and the loads for the one after
@@ -1471,9 +1380,12 @@ __global__ void __launch_bounds__(kScanThreads) gdn_chunk_scan_kernel(const GdnP
         }
         __syncthreads();  // the next chunk reads S0, its record, and rewrites dt
     }
-    if (!out_wave) {
+    {
+        const int v = tid >> 4, d0 = (tid & 15) * 4;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) *(f32x4 *)(state + (size_t)sv * kDk + 64 * tc + 16 * n + 4 * sl) = s0r[n];
+        for (int i = 0; i < 2; ++i) {
+            *(float4 *)(state + (size_t)v * kDk + d0 + 64 * i) = *(const float4 *)&L.s0[v][d0 + 64 * i];
+        }
     }
 }
 

@@ -6,6 +6,7 @@ plus the rows before it (src/model/native.rs:627-643, math.rs:102-155).  Each
 case is checked against the CPU oracle on the same seeded inputs with bf16 KV
 storage, at the bf16-path tolerance |d| <= 2e-3 + 1e-2 * |ref|.
 """
+import zlib
 import numpy as np
 import pytest
 
@@ -17,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def rng(request):
-    return np.random.default_rng(abs(hash(request.node.name)) % (2 ** 32))
+    return np.random.default_rng(zlib.crc32(request.node.name.encode()))
 
 
 @pytest.fixture(scope="module")

@@ -11,6 +11,7 @@ src/model/mtp.rs:110-112).  Row r of a sequence sees its context plus rows
 KV storage at |d| <= 2e-3 + 1e-2 * |ref|, and the kernels that ran are
 checked (no row falls back to the row-serial decode kernel).
 """
+import zlib
 import numpy as np
 import pytest
 
@@ -22,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def rng(request):
-    return np.random.default_rng(abs(hash(request.node.name)) % (2 ** 32))
+    return np.random.default_rng(zlib.crc32(request.node.name.encode()))
 
 
 def gammas(rng, dim):
