@@ -779,11 +779,7 @@ def bench_gdn_prefill(args, torch, pkg, steps, warmup):
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
         "gflop_per_step_token_serial": round(flops / 1e9, 2),
         "gflop_per_step_chunked_form": round(chunked_form / 1e9, 2),
-        # the state products run on split bf16 operands (hi + lo parts of every
-        # f32 operand, three bf16 MFMAs per product, exact products in f32);
-        # the state-independent prep on the f32 MFMA
-        "dtype": "f32 results: chunked WY form, prep on v_mfma_f32_16x16x4f32, scan on "
-                 "split-bf16 operands (v_mfma_f32_16x16x32_bf16, hi/lo parts)",
+        "dtype": "f32: chunked WY form, prep and scan on v_mfma_f32_16x16x4f32",
         "roofline": {
             # achieved: the reference's own (token-serial) f32 work over the
             # chunked kernels' time, against the f32 matrix peak: the arithmetic

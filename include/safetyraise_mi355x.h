@@ -314,8 +314,7 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_rollback(
  * sequence, run the recurrence token by token
  * (one workgroup per sequence and value head, state in registers); longer
  * calls with value_dim 128 and a 16-byte aligned qkv run the chunked (WY)
- * form in chunks of 32 rows (f32 MFMA, and bf16 MFMA on operands split in
- * two bf16 parts for the state products), which equals the token-serial
+ * form in chunks of 32 rows (f32 MFMA), which equals the token-serial
  * result within the f32 tolerance.  The chunked form keeps 68 KB of device
  * scratch per (32-row chunk, value head) of the call in the context's
  * staging buffer (e.g. 280 MB for 4096 rows at 32 value heads), grown on
