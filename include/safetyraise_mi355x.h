@@ -114,7 +114,7 @@ typedef struct safetyraise_kernel_kv_pool safetyraise_kernel_kv_pool;
 typedef struct safetyraise_kernel_kv_options {
     uint32_t struct_size;   /* sizeof(safetyraise_kernel_kv_options) */
     uint32_t kv_heads;
-    uint32_t head_dim;      /* 64, 128 or 256 */
+    uint32_t head_dim;      /* 1..512 (64, 128 and 256 take the tuned kernels) */
     uint32_t page_tokens;   /* power of two >= 16 (reference: 64, state.rs:167) */
     uint64_t num_pages;     /* pages in the pool */
     uint64_t max_tokens;    /* per-sequence capacity (max_context) */
@@ -187,7 +187,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_read(
  * head_dim <= 128 and 64 at head_dim 256; more rows run as row slices, each
  * reading the cache once); 16 or more rows to the MFMA prefill kernels.
  * Query-head groups other than 1..8 heads per KV head and RoPE widths not a
- * multiple of 32 go row by row to the decode kernel.  A synchronous call whose verify or prefill rows
+ * multiple of 32 go row by row to the decode kernel.  Head widths other than
+ * 64, 128 and 256 (up to 512) take plain f32 kernels for every row: all rows
+ * appended, then one wave per (row, query head) over the visible keys.  A synchronous call whose verify or prefill rows
  * meet a K/V/q value beyond the fp16 range of the MFMA operands
  * (|x| >= 65520) recomputes those sequences on the f32 split-K path; an
  * asynchronous one reports it at the next synchronous call.
@@ -253,13 +255,14 @@ typedef struct safetyraise_kernel_gdn_options {
     uint32_t struct_size;
     uint32_t key_heads;
     uint32_t value_heads;
-    uint32_t key_dim;   /* 128 */
-    uint32_t value_dim; /* 128 */
+    uint32_t key_dim;   /* 1..512 (128 takes the tuned kernels) */
+    uint32_t value_dim; /* 1..512 (128, or a multiple of 16 at key_dim 128, tuned) */
     uint32_t conv_kernel;
     uint32_t max_sequences;
-    /* 0, or the most rows per sequence a KEEP_ROWS call may carry (<= 64,
-     * value_dim 128): every sequence then has two state buffers, so that
-     * gdn_rollback can return it to the state after any row of such a call. */
+    /* 0, or the most rows per sequence a KEEP_ROWS call may carry (<= 64; at
+     * key_dim 128 with value_dim a multiple of 16, value_dim must be 128):
+     * every sequence then has two state buffers, so that gdn_rollback can
+     * return it to the state after any row of such a call. */
     uint32_t keep_rows;
 } safetyraise_kernel_gdn_options;
 
@@ -318,7 +321,9 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_rollback(
  * result within the f32 tolerance.  The chunked form keeps 68 KB of device
  * scratch per (32-row chunk, value head) of the call in the context's
  * staging buffer (e.g. 280 MB for 4096 rows at 32 value heads), grown on
- * demand: OUT_OF_MEMORY when it cannot be. */
+ * demand: OUT_OF_MEMORY when it cannot be.  Other key widths, and value
+ * widths that are not a multiple of 16, run token by token in one workgroup
+ * per (sequence, value head) with the state rows in HBM (a wave per row). */
 typedef struct safetyraise_kernel_gdn_args {
     uint32_t struct_size;
     uint32_t flags;

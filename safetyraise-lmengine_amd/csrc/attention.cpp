@@ -103,6 +103,60 @@ int32_t run_prefill_pack(Ctx *ctx, AttnLaunch &a, const std::vector<SeqMeta> &pa
     return kOk;
 }
 
+// A call at a head width the tuned kernels are not built for: every row of
+// every sequence through the generic kernels (append all rows, then attend).
+// Ends the call as the routed path below does: lengths advanced, the output
+// copied back for host pointers, and on a synchronous error the lengths of
+// every sequence restored.
+int32_t generic_forward(Ctx *ctx, const safetyraise_kernel_attention_args &A, AttnLaunch &L,
+                        const std::vector<uint64_t> &row0, bool device, bool async,
+                        size_t out_bytes) {
+    auto *pool = A.kv;
+    std::vector<float> denom(A.rotary_dim / 2);
+    for (uint32_t i = 0; i < A.rotary_dim / 2; ++i) {
+        denom[i] = rope_denominator(A.rope_theta, i, A.rotary_dim);
+    }
+    L.rope_denom = denom.data();
+    std::vector<uint64_t> old_len(A.num_seqs);
+    TableBatch batch;
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        old_len[i] = pool->seqs[A.seq_ids[i]].len;
+        int32_t st = kv_prepare_append(ctx, pool, A.seq_ids[i], A.seq_rows[i], &batch);
+        if (st != kOk) {
+            kv_flush_table(ctx, pool, batch);
+            return st;
+        }
+    }
+    TableGuard table_guard{ctx, pool, batch};
+    int32_t st = kv_flush_table(ctx, pool, batch);
+    if (st != kOk) return st;
+    std::vector<SeqMeta> seqs(A.num_seqs);
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        SeqMeta m{};
+        m.slot = A.seq_ids[i];
+        m.ctx = (uint32_t)old_len[i];
+        m.rows = A.seq_rows[i];
+        m.row0 = (uint32_t)row0[i];
+        seqs[i] = m;
+    }
+    const hipError_t e = launch_attn_generic(ctx->stream, L, seqs.data(), (int)seqs.size());
+    if (e != hipSuccess) return hip_fail(ctx, e, "generic attention launch");
+    for (uint32_t i = 0; i < A.num_seqs; ++i) {
+        pool->seqs[A.seq_ids[i]].len = old_len[i] + A.seq_rows[i];
+    }
+    if (!device) {
+        SR_HIP(ctx, hipMemcpyAsync(A.out, L.out, out_bytes, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    table_guard.armed = false;
+    st = finish_call(ctx, async);
+    if (st != kOk && !async) {
+        for (uint32_t i = 0; i < A.num_seqs; ++i) {
+            pool->seqs[A.seq_ids[i]].len = old_len[i];
+        }
+    }
+    return st;
+}
+
 }  // namespace
 
 int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args *args,
@@ -233,6 +287,10 @@ int32_t attention_forward_impl(Ctx *ctx, const safetyraise_kernel_attention_args
         L.q_norm = qk_norm ? (const float *)(base + regions[4].offset) : nullptr;
         L.k_norm = qk_norm ? (const float *)(base + regions[5].offset) : nullptr;
         L.out = (float *)(base + out_off);
+    }
+
+    if (generic_head_dim(A.head_dim)) {
+        return generic_forward(ctx, A, L, row0, device, async, out_bytes);
     }
 
     // Routing (below): 16+ rows -> prefill, 2..15 supported rows -> verify,

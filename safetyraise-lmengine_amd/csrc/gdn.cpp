@@ -61,15 +61,18 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_create(
     }
     const auto &o = *options;
     if (o.key_heads == 0 || o.value_heads == 0 || o.value_heads % o.key_heads != 0 ||
-        o.key_dim != gdn_key_dim() || o.value_dim == 0 || o.value_dim % gdn_row_block() != 0 ||
+        o.key_dim == 0 || o.key_dim > kGdnMaxDim || o.value_dim == 0 || o.value_dim > kGdnMaxDim ||
         o.conv_kernel == 0 || o.conv_kernel > gdn_max_kernel() || o.max_sequences == 0 ||
         o.max_sequences > 65536) {
         return fail(context, kInvalid,
-                    "GDN geometry is invalid (key_dim 128, value_dim a multiple of 16, "
-                    "value_heads a multiple of key_heads, conv kernel 1..8)");
+                    "GDN geometry is invalid (key_dim and value_dim 1..512, value_heads a "
+                    "multiple of key_heads, conv kernel 1..8)");
     }
-    if (o.keep_rows > kMaxKeepRows || (o.keep_rows > 0 && o.value_dim != 128)) {
-        return fail(context, kInvalid, "GDN keep_rows must be at most 64, with value_dim 128");
+    if (o.keep_rows > kMaxKeepRows ||
+        (o.keep_rows > 0 && o.value_dim % gdn_row_block() == 0 && o.key_dim == gdn_key_dim() &&
+         o.value_dim != 128)) {
+        return fail(context, kInvalid,
+                    "GDN keep_rows must be at most 64 (value_dim 128 at key_dim 128)");
     }
     Pool *pool = new (std::nothrow) Pool();
     if (pool == nullptr) return fail(context, kNoMemory, "gdn pool allocation failed");
@@ -399,6 +402,8 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_gdn_rollback(
         r.value_heads = pool->value_heads;
         r.channels = pool->channels;
         r.conv_k = pool->conv_kernel;
+        r.key_dim = pool->key_dim;
+        r.value_dim = pool->value_dim;
         SR_HIP(ctx, launch_gdn_rollback(ctx->stream, r));
         pool->kept_at[sequence] = rows;
     }

@@ -1511,17 +1511,223 @@ __global__ void __launch_bounds__(256) gdn_norm_gate_kernel(const NormParams p) 
     }
 }
 
+// ---------------------------------------------------------------------------
+// gdn_generic_kernel: key and value widths the tuned kernels are not built
+// for (key_dim other than 128, value_dim not a multiple of 16; up to
+// kGdnMaxDim each).  One workgroup of 256 threads per (value head, sequence),
+// token by token as math.rs:190-239: the head's conv channels (q and k of its
+// key head, its v) and their history in LDS; the L2 norms of q and k; the
+// delta rule with a wave per state row (lanes over the key dims, so every
+// state access is a contiguous run of the row) in the order decay, predict,
+// correct, read; the raw outputs go to raw_out for gdn_norm_gate_kernel.
+// KEEP_ROWS records as gdn_head_kernel writes them.
+// ---------------------------------------------------------------------------
+constexpr int kGenThreads = 256;
+constexpr uint32_t kGenKeysPerLane = kGdnMaxDim / 64;
+
+// Sum over the 256 threads; every thread gets the total.  red holds 4 floats.
+__device__ __forceinline__ float block_sum256(float x, float *red) {
+    x = sum64(x);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return t;
+}
+
+__global__ void __launch_bounds__(kGenThreads) gdn_generic_kernel(const GdnParams p,
+                                                                   uint32_t key_dim) {
+    extern __shared__ float gsh[];
+    const uint32_t Dk = key_dim, Dv = p.value_dim;
+    const uint32_t K = p.conv_k, K1 = K - 1;
+    const uint32_t hch = 2 * Dk + Dv;  // q, k and v channels of the head
+    float *conv_s = gsh;               // [hch] the row's conv outputs
+    float *hist_s = gsh + hch;         // [hch][K-1] raw inputs, oldest first
+    __shared__ float red_s[4];
+    __shared__ float qk_s[2];
+    __shared__ float ab_s[2];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t h = blockIdx.x;
+    const GdnMeta m = p.meta[blockIdx.y];
+    const uint32_t groups = p.value_heads / p.key_heads;
+    const uint32_t kh = h / groups;
+    const uint32_t key_width = p.key_heads * Dk;
+    const bool bf16_in = p.bf16_in != 0;
+    auto chan = [&](uint32_t c) -> uint32_t {
+        if (c < Dk) return kh * Dk + c;
+        if (c < 2 * Dk) return key_width + kh * Dk + (c - Dk);
+        return 2 * key_width + h * Dv + (c - 2 * Dk);
+    };
+    const size_t hist_slot = ((size_t)m.parity * p.max_slots + m.slot) * p.channels;
+    const size_t hist_next = ((size_t)(1 - m.parity) * p.max_slots + m.slot) * p.channels;
+    for (uint32_t c = tid; c < hch; c += kGenThreads) {
+        for (uint32_t j = 0; j < K1; ++j) hist_s[c * K1 + j] = p.history[(hist_slot + chan(c)) * K1 + j];
+    }
+    const float a_log_e = expf(p.a_log[h]);
+    const float dt = p.dt_bias[h];
+    const float qscale = 1.0f / sqrtf((float)Dk);  // math.rs:213
+    const float *s_in = p.state + ((size_t)m.state_in * p.value_heads + h) * Dv * Dk;
+    float *s_out = p.state + ((size_t)m.state_out * p.value_heads + h) * Dv * Dk;
+    const bool keep = p.records != nullptr;
+    const uint32_t hv_dv = p.value_heads * Dv;
+    const size_t rec_k = p.value_heads + hv_dv;                  // k^ [Hv][Dk]
+    const size_t rec_x = rec_k + (size_t)p.value_heads * Dk;     // raw inputs [C]
+    const bool owns_qk = (h % groups == 0);
+    __syncthreads();
+
+    for (uint32_t r = 0; r < m.rows; ++r) {
+        const size_t row = (size_t)m.row0 + r;
+        float *rec = keep ? p.records + ((size_t)m.slot * p.keep_rows + r) * p.rec_stride : nullptr;
+        // A. causal conv + silu (math.rs:175-185), history shifted in LDS
+        for (uint32_t c = tid; c < hch; c += kGenThreads) {
+            const uint32_t ch = chan(c);
+            const float x = load_act(p.qkv, row * p.channels + ch, bf16_in);
+            const float *w = p.conv_w + (size_t)ch * K;
+            float acc = 0.0f;
+            for (uint32_t j = 0; j < K1; ++j) acc += hist_s[c * K1 + j] * w[j];
+            const float value = acc + x * w[K1];
+            conv_s[c] = value * ref_sigmoid(value);
+            for (uint32_t j = 0; j + 1 < K1; ++j) hist_s[c * K1 + j] = hist_s[c * K1 + j + 1];
+            if (K1 > 0) hist_s[c * K1 + K1 - 1] = x;
+            if (keep && (c >= 2 * Dk || owns_qk)) rec[rec_x + ch] = x;
+        }
+        if (tid == 0) {
+            // math.rs:220-221
+            const float av = load_act(p.a, row * p.value_heads + h, bf16_in);
+            const float bv = load_act(p.b, row * p.value_heads + h, bf16_in);
+            ab_s[0] = expf(-a_log_e * softplus_ref(av + dt));
+            ab_s[1] = ref_sigmoid(bv);
+            if (keep) rec[h] = ab_s[0];
+        }
+        __syncthreads();
+        // B. L2 norms of q and k (math.rs:218-219)
+        float sq = 0.0f, sk = 0.0f;
+        for (uint32_t d = tid; d < Dk; d += kGenThreads) {
+            sq += conv_s[d] * conv_s[d];
+            sk += conv_s[Dk + d] * conv_s[Dk + d];
+        }
+        sq = block_sum256(sq, red_s);
+        sk = block_sum256(sk, red_s);
+        if (tid == 0) {
+            qk_s[0] = 1.0f / sqrtf(sq + 1e-6f);
+            qk_s[1] = 1.0f / sqrtf(sk + 1e-6f);
+        }
+        __syncthreads();
+        const float qi = qk_s[0], ki = qk_s[1];
+        const float alpha = ab_s[0], beta = ab_s[1];
+        float kh[kGenKeysPerLane], qh[kGenKeysPerLane];
+#pragma unroll
+        for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+            const uint32_t d = lane + 64 * i;
+            kh[i] = d < Dk ? conv_s[Dk + d] * ki : 0.0f;
+            qh[i] = d < Dk ? conv_s[d] * qi : 0.0f;
+            if (keep && wave == 0 && d < Dk) rec[rec_k + (size_t)h * Dk + d] = kh[i];
+        }
+        // C. delta rule, a wave per state row (math.rs:222-236)
+        const float *src = r == 0 ? s_in : s_out;
+        for (uint32_t v = wave; v < Dv; v += kGenThreads / 64) {
+            const float *srow = src + (size_t)v * Dk;
+            float *drow = s_out + (size_t)v * Dk;
+            float sv[kGenKeysPerLane];
+            float pred = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+                const uint32_t d = lane + 64 * i;
+                sv[i] = d < Dk ? srow[d] * alpha : 0.0f;
+                pred += sv[i] * kh[i];
+            }
+            pred = sum64(pred);
+            const float corr = beta * (conv_s[2 * Dk + v] - pred);
+            if (keep && lane == 0) rec[p.value_heads + (size_t)h * Dv + v] = corr;
+            float rd = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+                const uint32_t d = lane + 64 * i;
+                sv[i] = fmaf(corr, kh[i], sv[i]);
+                rd += sv[i] * qh[i];
+                if (d < Dk) drow[d] = sv[i];
+            }
+            rd = sum64(rd);
+            if (lane == 0) p.raw_out[row * hv_dv + (size_t)h * Dv + v] = rd * qscale;
+        }
+        __syncthreads();  // conv_s is rewritten by the next row
+    }
+    // next history: v channels here; q/k channels by the first value head of
+    // the key group (the others hold the same values)
+    for (uint32_t c = tid; c < hch; c += kGenThreads) {
+        if (c < 2 * Dk && !owns_qk) continue;
+        for (uint32_t j = 0; j < K1; ++j) p.history[(hist_next + chan(c)) * K1 + j] = hist_s[c * K1 + j];
+    }
+}
+
+// gdn_rollback_kernel for the widths of gdn_generic_kernel: the state after
+// row `keep` rebuilt with the forward's own operations (a product by the
+// decay, then a fused multiply-add of the correction), a wave per state row.
+struct RollbackGenericParams {
+    RollbackParams r;
+    uint32_t key_dim, value_dim;
+};
+
+__global__ void __launch_bounds__(256) gdn_rollback_generic_kernel(const RollbackGenericParams q) {
+    const RollbackParams &p = q.r;
+    const uint32_t Dk = q.key_dim, Dv = q.value_dim;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t hv_dv = p.value_heads * Dv;
+    const size_t rec_k = p.value_heads + hv_dv;
+    const size_t rec_x = rec_k + (size_t)p.value_heads * Dk;
+    if (blockIdx.x < p.value_heads) {
+        const uint32_t h = blockIdx.x;
+        for (uint32_t v = wave; v < Dv; v += 4) {
+            const float *src = p.state_in + ((size_t)h * Dv + v) * Dk;
+            float *dst = p.state_out + ((size_t)h * Dv + v) * Dk;
+            float sv[kGenKeysPerLane];
+#pragma unroll
+            for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+                const uint32_t d = lane + 64 * i;
+                sv[i] = d < Dk ? src[d] : 0.0f;
+            }
+            for (uint32_t r = 0; r < p.keep; ++r) {
+                const float *rec = p.records + (size_t)r * p.rec_stride;
+                const float alpha = rec[h];
+                const float corr = rec[p.value_heads + (size_t)h * Dv + v];
+#pragma unroll
+                for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+                    const uint32_t d = lane + 64 * i;
+                    const float khd = d < Dk ? rec[rec_k + (size_t)h * Dk + d] : 0.0f;
+                    sv[i] = fmaf(corr, khd, sv[i] * alpha);
+                }
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < kGenKeysPerLane; ++i) {
+                const uint32_t d = lane + 64 * i;
+                if (d < Dk) dst[d] = sv[i];
+            }
+        }
+        return;
+    }
+    const uint32_t c = (blockIdx.x - p.value_heads) * 256 + tid;
+    const uint32_t K1 = p.conv_k - 1;
+    if (c >= p.channels || K1 == 0) return;
+    for (uint32_t i = 0; i < K1; ++i) {
+        const uint32_t t = p.keep + i;
+        p.hist_out[(size_t)c * K1 + i] =
+            t < K1 ? p.hist_in[(size_t)c * K1 + t]
+                   : p.records[(size_t)(t - K1) * p.rec_stride + rec_x + c];
+    }
+}
+
 // Which kernels a call takes.  Decode-sized calls (at most kHeadKernelRows
 // rows per sequence) run one workgroup per (sequence, value head) with the
 // norm and gate fused, and so do KEEP_ROWS calls (records of every row).
 // Longer calls with Dv = 128 take the chunked MFMA form, which reads the qkv
 // rows in 16-byte segments; the rest the token-serial row-block kernel.
-enum class GdnRoute { kHead, kChunk, kDelta };
+enum class GdnRoute { kHead, kChunk, kDelta, kGeneric };
 
 GdnRoute gdn_route(const safetyraise_kernel_gdn_pool *pool, const GdnSeq *seqs, int nseq,
                    bool keep, bool qkv_aligned) {
     uint32_t max_rows = 0;
     for (int i = 0; i < nseq; ++i) max_rows = seqs[i].rows > max_rows ? seqs[i].rows : max_rows;
+    if (pool->key_dim != kDk || pool->value_dim % kRows != 0) return GdnRoute::kGeneric;
     if (pool->value_dim == kHeadDv && (max_rows <= kHeadKernelRows || keep)) return GdnRoute::kHead;
     if (pool->value_dim == kHeadDv && qkv_aligned) return GdnRoute::kChunk;
     return GdnRoute::kDelta;
@@ -1546,8 +1752,10 @@ size_t gdn_chunk_rec_bytes(const safetyraise_kernel_gdn_pool *pool, const GdnSeq
 hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs, int nseq,
                       uint32_t total_rows) {
     const auto *pool = g.pool;
-    if (g.keep && pool->value_dim != kHeadDv) return hipErrorInvalidValue;
     const GdnRoute route = gdn_route(pool, seqs, nseq, g.keep, ((uintptr_t)g.qkv & 15) == 0);
+    if (g.keep && route != GdnRoute::kHead && route != GdnRoute::kGeneric) {
+        return hipErrorInvalidValue;
+    }
     const bool head_kernel = route == GdnRoute::kHead;
     const bool chunk_kernel = route == GdnRoute::kChunk;
     if (chunk_kernel && g.chunk_rec == nullptr) return hipErrorInvalidValue;
@@ -1592,6 +1800,11 @@ hipError_t launch_gdn(hipStream_t stream, const GdnLaunch &g, const GdnSeq *seqs
                 SR_LAUNCH("gdn_head_kernel", (gdn_head_kernel<kHeadThreads, ConvChan>), grid,
                           dim3(kHeadThreads), 0, stream, p, g.norm, g.z, g.out, g.err_word, g.eps);
             }
+        } else if (route == GdnRoute::kGeneric) {
+            const uint32_t hch = 2 * pool->key_dim + pool->value_dim;
+            const size_t lds = (size_t)hch * pool->conv_kernel * sizeof(float);
+            SR_LAUNCH("gdn_generic_kernel", gdn_generic_kernel, dim3(pool->value_heads, (uint32_t)n),
+                      dim3(kGenThreads), lds, stream, p, pool->key_dim);
         } else if (chunk_kernel) {
             const hipError_t e =
                 launch_chunk(stream, p, max_chunks, (uint64_t)chunks * pool->value_heads, g.num_cus);
@@ -1637,7 +1850,13 @@ hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r) {
     p.channels = r.channels;
     p.conv_k = r.conv_k;
     const uint32_t blocks = r.value_heads + (r.channels + 255) / 256;
-    SR_LAUNCH("gdn_rollback_kernel", gdn_rollback_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    if (r.key_dim == kDk && r.value_dim == kHeadDv) {
+        SR_LAUNCH("gdn_rollback_kernel", gdn_rollback_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    } else {
+        const RollbackGenericParams q{p, r.key_dim, r.value_dim};
+        SR_LAUNCH("gdn_rollback_generic_kernel", gdn_rollback_generic_kernel, dim3(blocks),
+                  dim3(256), 0, stream, q);
+    }
     return hipGetLastError();
 }
 

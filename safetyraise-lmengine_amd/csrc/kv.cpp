@@ -124,12 +124,12 @@ SAFETYRAISE_KERNEL_EXPORT int32_t safetyraise_kernel_kv_create(
         return fail(context, kInvalid, "kv options pointer or struct_size is invalid");
     }
     const auto &o = *options;
-    if (o.kv_heads == 0 || (o.head_dim != 64 && o.head_dim != 128 && o.head_dim != 256) ||
+    if (o.kv_heads == 0 || o.head_dim == 0 || o.head_dim > kGenericMaxHeadDim ||
         o.page_tokens < 16 || o.page_tokens > 65536 || (o.page_tokens & (o.page_tokens - 1)) != 0 ||
         o.num_pages == 0 || o.num_pages > INT32_MAX || o.max_tokens == 0 ||
         o.max_tokens > INT32_MAX || o.max_sequences == 0 || o.max_sequences > (1u << 20)) {
         return fail(context, kInvalid,
-                    "kv geometry is invalid (head_dim 64/128/256, page_tokens a power of two in "
+                    "kv geometry is invalid (head_dim 1..512, page_tokens a power of two in "
                     "16..65536, non-zero sizes)");
     }
     uint64_t page_elems, bytes, table;

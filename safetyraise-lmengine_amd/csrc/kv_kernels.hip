@@ -93,6 +93,29 @@ __global__ void kv_scatter_kernel(const ScatterParams p) {
     }
 }
 
+// One thread per value: head widths that are not a multiple of 8 (a run of
+// 8 values would straddle two heads or start off a 16-byte boundary).
+__global__ void kv_scatter_elem_kernel(const ScatterParams p) {
+    const uint64_t width = (uint64_t)p.kv_heads * p.head_dim;
+    const uint64_t n = p.tokens * width;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t t = i / width;
+        const uint32_t r = (uint32_t)(i % width);
+        const uint32_t h = r / p.head_dim;
+        const uint32_t d = r % p.head_dim;
+        const uint64_t tok = p.start + t;
+        const int32_t page = p.table[tok / p.page_tokens];
+        const size_t dst =
+            (((size_t)h * p.num_pages + page) * p.page_tokens + tok % p.page_tokens) * p.head_dim + d;
+        const float k = load_act(p.keys, i, p.bf16_in != 0);
+        const float v = load_act(p.values, i, p.bf16_in != 0);
+        if (!isfinite(k) || !isfinite(v)) atomicOr(p.err_word, kErrNonFiniteKv);
+        p.k_pages[dst] = f32_to_bf16(k);
+        p.v_pages[dst] = f32_to_bf16(v);
+    }
+}
+
 struct GatherParams {
     const uint16_t *k_pages;
     const uint16_t *v_pages;
@@ -167,8 +190,17 @@ hipError_t launch_kv_scatter(hipStream_t s, const safetyraise_kernel_kv_pool *po
     p.head_dim = pool->head_dim;
     p.page_tokens = pool->page_tokens;
     p.bf16_in = bf16_in ? 1 : 0;
-    const uint64_t work = tokens * pool->kv_heads * (pool->head_dim / 8);
-    SR_LAUNCH("kv_scatter_kernel", kv_scatter_kernel, dim3(grid_for(work, 256)), dim3(256), 0, s, p);
+    // (the callers pass 16-byte aligned rows: kv_append checks device
+    // pointers, host inputs are staged at 256-byte offsets)
+    if (pool->head_dim % 8 == 0) {
+        const uint64_t work = tokens * pool->kv_heads * (pool->head_dim / 8);
+        SR_LAUNCH("kv_scatter_kernel", kv_scatter_kernel, dim3(grid_for(work, 256)), dim3(256), 0,
+                  s, p);
+    } else {
+        const uint64_t work = tokens * pool->kv_heads * pool->head_dim;
+        SR_LAUNCH("kv_scatter_elem_kernel", kv_scatter_elem_kernel, dim3(grid_for(work, 256)),
+                  dim3(256), 0, s, p);
+    }
     return hipGetLastError();
 }
 

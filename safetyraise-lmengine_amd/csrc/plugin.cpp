@@ -159,12 +159,16 @@ static void destroy_timer_events(KernelTimer &t) {
     t.used = 0;
 }
 
+float rope_denominator(float theta, uint32_t i, uint32_t rotary_dim) {
+    // src/model/math.rs:90-91: theta.powf((2*i) as f32 / rotary_dim as f32)
+    const float exponent = (float)(2 * i) / (float)rotary_dim;
+    return powf(theta, exponent);
+}
+
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim) {
     if (ctx->rope_theta != theta || ctx->rope_dim != rotary_dim) {
         for (uint32_t i = 0; i < rotary_dim / 2 && i < 128; ++i) {
-            // src/model/math.rs:90-91: theta.powf((2*i) as f32 / rotary_dim as f32)
-            const float exponent = (float)(2 * i) / (float)rotary_dim;
-            ctx->rope.denom[i] = powf(theta, exponent);
+            ctx->rope.denom[i] = rope_denominator(theta, i, rotary_dim);
         }
         ctx->rope_theta = theta;
         ctx->rope_dim = rotary_dim;

@@ -32,6 +32,11 @@ constexpr uint32_t kErrPrefillRange = 4u;
 
 // Sequences per kernel launch whose metadata travels in the kernel arguments.
 constexpr int kMetaPerLaunch = 64;
+// Widest attention head the generic kernels take (head widths other than 64,
+// 128 and 256; attn_generic.hip).
+constexpr uint32_t kGenericMaxHeadDim = 512;
+// Widest GDN key or value head the generic kernels take (gdn_kernels.hip).
+constexpr uint32_t kGdnMaxDim = 512;
 
 // Grow-only device allocation owned by a context.
 struct DeviceBuffer {
@@ -215,6 +220,8 @@ int32_t take_error_word(Ctx *ctx, uint32_t *word);
 // The status and message for a non-zero error word.
 int32_t error_word_status(Ctx *ctx, uint32_t word);
 const RopeTable &rope_table(Ctx *ctx, float theta, uint32_t rotary_dim);
+// theta^(2i/rotary_dim) as math.rs:90-91 computes it (C library powf, f32)
+float rope_denominator(float theta, uint32_t i, uint32_t rotary_dim);
 
 // KV pool helpers used by attention.  Page-table entries changed by
 // kv_prepare_append are queued in `batch` when it is given (and uploaded by
@@ -254,6 +261,9 @@ struct AttnLaunch {
     float *out;
     uint32_t *err_word;
     const RopeTable *rope;
+    // generic head widths: theta^(2i/rotary_dim) for i < rotary_dim/2 (up to
+    // kGenericMaxHeadDim/2 pairs, more than RopeTable holds)
+    const float *rope_denom = nullptr;
     // page-table entries of this call not yet on the device (at most
     // kInlineTable): the first append kernel of the call writes them, and
     // resolves its own rows' pages from them
@@ -306,6 +316,11 @@ hipError_t launch_attn_prefill(hipStream_t s, const AttnLaunch &a, const SeqMeta
 // head_dim <= 128): split-K over key partitions with MFMA inner products,
 // then a combine pass; partial records come from in.reserve_partials.
 bool verify_supported(const AttnLaunch &a, uint32_t rows);
+// Head widths other than 64, 128 and 256 (up to kGenericMaxHeadDim): every
+// row of the call through the plain f32 kernels of attn_generic.hip (append,
+// then attention); a.rope_denom must hold the rotary pairs' denominators.
+bool generic_head_dim(uint32_t head_dim);
+hipError_t launch_attn_generic(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq);
 hipError_t launch_attn_verify(hipStream_t s, const AttnLaunch &a, const SeqMeta *seqs, int nseq,
                               void *rope_scratch, const DecodePlanInput &in);
 
@@ -342,6 +357,7 @@ struct GdnRollback {
     float *hist_out;
     const float *records;
     uint32_t rec_stride, keep, value_heads, channels, conv_k;
+    uint32_t key_dim, value_dim;
 };
 hipError_t launch_gdn_rollback(hipStream_t stream, const GdnRollback &r);
 

@@ -161,7 +161,11 @@ def test_gdn_error_paths(pkg, backend, rng):
     with pytest.raises(pkg.PluginError):
         pkg.GdnState(backend, 2, 3, 128, 16, 4, 1)   # value_heads % key_heads
     with pytest.raises(pkg.PluginError):
-        pkg.GdnState(backend, 1, 1, 64, 16, 4, 1)    # key_dim must be 128
+        pkg.GdnState(backend, 1, 1, 600, 16, 4, 1)   # key_dim above 512
+    with pytest.raises(pkg.PluginError):
+        pkg.GdnState(backend, 1, 1, 128, 0, 4, 1)    # empty value heads
+    with pytest.raises(pkg.PluginError):
+        pkg.GdnState(backend, 1, 1, 128, 16, 9, 1)   # conv kernel above 8
     L = Layer(rng, 1, 1, 128, 16, 4)
     pool = pkg.GdnState(backend, 1, 1, 128, 16, 4, 1)
     s = pool.open()
