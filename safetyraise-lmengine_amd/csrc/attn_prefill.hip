@@ -610,6 +610,63 @@ struct LeanIo {
             return (((head_base + (uint32_t)table[tok >> lpt]) << lpt) + (tok & pt_mask)) * D;
         }
     }
+    // kTilePage: the thread's rows of a tile as byte offsets from the tile's
+    // first key (the same for every tile, so computed once), and the tile's
+    // first byte from a wave-uniform page id.  With the page id in a scalar
+    // register the tile pointer is scalar too, and each row load is one
+    // global load with a 32-bit vector offset: no 64-bit address arithmetic
+    // in the vector unit per tile.
+    __device__ __forceinline__ void tile_offsets(uint32_t gt, uint32_t (&off)[KL]) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) off[i] = ((k0 + i * KSTEP) * D + ch * 8) * 2;
+    }
+    __device__ __forceinline__ const unsigned char *tile_ptr(const uint16_t *src, uint32_t t,
+                                                             uint32_t pg) const {
+        return (const unsigned char *)(src + (((head_base + pg) << lpt) +
+                                              ((t * kKeyTile) & pt_mask)) * D);
+    }
+    template <int N>
+    __device__ __forceinline__ void load_rows(u32x4 (&r)[N], const unsigned char *tile,
+                                              const uint32_t (&off)[KL]) const {
+        static_assert(N >= KL, "staging registers");
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            // the 32-bit offset is materialised here, so the address stays
+            // (scalar pointer + zero-extended vector offset), the form of a
+            // global load with a scalar base, instead of a hoisted 64-bit
+            // vector value added per load
+            uint32_t o = off[i];
+            pin(o);
+            r[i] = *(const u32x4 *)(tile + o);
+        }
+    }
+    // LDS byte offsets of the thread's rows in the K image (is_v false) or
+    // the row-major V image (is_v true); computed once
+    __device__ __forceinline__ void lds_offsets(uint32_t gt, bool is_v, uint32_t (&off)[KL]) const {
+        const uint32_t ch = gt % KCH, k0 = gt / KCH;
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            const uint32_t key = k0 + i * KSTEP;
+            off[i] = key * (D * 2) + ((ch ^ (is_v ? v_swz(k0) : k_swz<D>(key))) * 16);
+        }
+    }
+    // store_k / store_v_rows with the offsets of lds_offsets; rows from
+    // valid_keys on (V only, a partial last tile) become 0
+    template <int N>
+    __device__ __forceinline__ void store_rows(const u32x4 (&r)[N], unsigned char *buf,
+                                               const uint32_t (&off)[KL], uint32_t k0,
+                                               uint32_t valid_keys) const {
+        const bool partial = valid_keys < (uint32_t)kKeyTile;  // uniform
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(r[i][j]), bf16hi(r[i][j]));
+            if (partial && k0 + i * KSTEP >= valid_keys) f = u32x4{0, 0, 0, 0};
+            *(u32x4 *)(buf + off[i]) = f;
+        }
+    }
     template <int N>
     __device__ __forceinline__ void load_k(u32x4 (&r)[N], uint32_t t, size_t base, uint32_t gt) const {
         static_assert(N >= KL, "staging registers");
@@ -1420,6 +1477,23 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     Io io;
     io.init(p, b);
     const uint32_t gt0 = tid & 255;
+    // kTilePage: this thread's row offsets in a global tile and in its
+    // group's LDS image (K for group 0, V for group 1), computed once; the
+    // group's source pages and LDS image are wave-uniform
+    uint32_t goff[SL] = {}, loff[SL] = {};
+    const uint32_t k0 = gt0 / Io::KCH;
+    if constexpr (kTilePage) {
+        io.tile_offsets(gt0, goff);
+        io.lds_offsets(gt0, grp != 0, loff);
+    }
+    const uint16_t *src_pages = grp != 0 ? p.v_pages : p.k_pages;
+    unsigned char *img = grp != 0 ? vbuf : kbuf;
+    // tile t's first byte from its page id, in scalar registers at this point
+    auto tile_at = [&](uint32_t t, uint32_t pg) __attribute__((always_inline)) {
+        uint64_t tp = (uint64_t)io.tile_ptr(src_pages, t, __builtin_amdgcn_readfirstlane(pg));
+        pin_s(tp);
+        return global_from_bits<const unsigned char>(tp);
+    };
     // staging registers, two sets: tile j's data lives in stage[j & 1], so a
     // load never waits for the LDS stores that read the other set
     u32x4 stage0[SL] = {}, stage1[SL] = {};
@@ -1429,7 +1503,11 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     // issued after it, and a wait that must also cover this path can then
     // still leave those loads in flight.
     uint32_t pg_next = io.page_of(2);
-    {
+    if constexpr (kTilePage) {
+        const uint32_t pg0 = io.page_of(0), pg1 = io.page_of(1);
+        io.load_rows(stage0, tile_at(0, pg0), goff);
+        io.load_rows(stage1, tile_at(min(1u, n - 1), pg1), goff);
+    } else {
         const uint32_t pg0 = io.page_of(0), pg1 = io.page_of(1);
         const size_t tb0 = io.tile_base(0, pg0), tb1 = io.tile_base(min(1u, n - 1), pg1);
         io.load_kv(stage0, 0, tb0, gt0, grp != 0);
@@ -1468,8 +1546,12 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     } else {
         q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop);
     }
-    if (grp == 0) io.store_k(stage0, kbuf, gt0);
-    else io.store_v_rows(stage0, vbuf, b.n_keys, gt0);
+    if constexpr (kTilePage) {
+        io.store_rows(stage0, img, loff, k0, grp != 0 ? b.n_keys : (uint32_t)kKeyTile);
+    } else {
+        if (grp == 0) io.store_k(stage0, kbuf, gt0);
+        else io.store_v_rows(stage0, vbuf, b.n_keys, gt0);
+    }
     uint32_t voff[NT];
     pv_rows_offsets<D>(lane, voff);
     f32x16 oacc[NT];
@@ -1499,23 +1581,38 @@ attn_prefill_pp_kernel(const PrefillParams p) {
         // here, before this phase's LDS stores are issued, so that its wait
         // does not also wait for them.  Then tile t+3's is requested.
         const uint32_t t_next = min(t + 2, n - 1);
-        size_t tb_next = io.tile_base(t_next, pg_next);
-        pin(tb_next);
+        const unsigned char *tile_next = nullptr;
+        size_t tb_next = 0;
+        if constexpr (kTilePage) {
+            tile_next = tile_at(t_next, pg_next);
+        } else {
+            tb_next = io.tile_base(t_next, pg_next);
+            pin(tb_next);
+        }
         pg_next = io.page_of(t + 3);
         const uint32_t key0 = t * kKeyTile;
         softmax_tile_ref<D, MASKED>(sacc, key0, key_limit, h, t == 0, m_run, negm, l_run, oacc,
                                     pop);
-        uint32_t gt = gt0;
-        pin(gt);
-        if (t + 1 < n) {
-            if (grp == 0) io.store_k(cur, kbuf + (PAR ^ 1) * kTileBytes<D>, gt);
-            else io.store_v_rows(cur, vbuf + (PAR ^ 1) * kTileBytes<D>,
-                                 MASKED ? b.n_keys - key0 - kKeyTile : (uint32_t)kKeyTile, gt);
+        if constexpr (kTilePage) {
+            if (t + 1 < n) {
+                io.store_rows(cur, img + (PAR ^ 1) * kTileBytes<D>, loff, k0,
+                              (MASKED && grp != 0) ? b.n_keys - key0 - kKeyTile
+                                                   : (uint32_t)kKeyTile);
+            }
+            // issued on every path (past the end, the last tile again): a
+            // load skipped on some path would make the next wait for an older
+            // load (the page id) wait for every load in flight
+            io.load_rows(nxt, tile_next, goff);
+        } else {
+            uint32_t gt = gt0;
+            pin(gt);
+            if (t + 1 < n) {
+                if (grp == 0) io.store_k(cur, kbuf + (PAR ^ 1) * kTileBytes<D>, gt);
+                else io.store_v_rows(cur, vbuf + (PAR ^ 1) * kTileBytes<D>,
+                                     MASKED ? b.n_keys - key0 - kKeyTile : (uint32_t)kKeyTile, gt);
+            }
+            io.load_kv(nxt, t_next, tb_next, gt, grp != 0);
         }
-        // issued on every path (past the end, the last tile again): a load
-        // skipped on some path would make the next wait for an older load
-        // (the page id) wait for every load in flight
-        io.load_kv(nxt, t_next, tb_next, gt, grp != 0);
         // the softmax results stay in this phase
 #pragma unroll
         for (int st = 0; st < 4; ++st) pin(pop[st]);
