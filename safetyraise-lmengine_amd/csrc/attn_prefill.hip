@@ -1765,8 +1765,11 @@ constexpr uint32_t kVerifyPageSlots = 2048;
 // and row addresses and staging it costs no more than staging K) or as V^T
 // with vt_swz (D = 64).  Every offset is recomputed from gt at each use, so
 // that only the tiles in flight occupy registers.  Page ids come from the
-// partition's LDS copy.
-template <int D>
+// partition's LDS copy.  kShared: the partition's tiles are read by more
+// than one workgroup (row slices, dispatched together on one XCD), so the
+// loads are ordinary ones that leave the lines in L2 for the sibling slices;
+// otherwise every tile is read once and the loads are nontemporal.
+template <int D, bool kShared = false>
 struct VerifyIo {
     static constexpr bool kRowV = D >= 128;
     static constexpr int NL = D <= 128 ? 128 : 256;         // lanes staging one tile
@@ -1808,21 +1811,25 @@ struct VerifyIo {
             for (int i = 0; i < VL; ++i) pv[i] = (uint32_t)pids[(tv[i] >> lpt) - first];
         }
         __builtin_amdgcn_sched_barrier(0);
-        // every tile is read by one workgroup once: nontemporal loads
-        // (streaming reads measured ~8 % faster than ordinary loads)
+        // a tile read by one workgroup once: nontemporal loads (streaming
+        // reads measured ~8 % faster than ordinary loads)
+        auto ld = [](const u32x4 *a) __attribute__((always_inline)) {
+            if constexpr (kShared) return *a;
+            else return __builtin_nontemporal_load(a);
+        };
 #pragma unroll
-        for (int i = 0; i < KL; ++i) kr[i] = __builtin_nontemporal_load(row_ptr(k_head, pk[i], tk[i], ch));
+        for (int i = 0; i < KL; ++i) kr[i] = ld(row_ptr(k_head, pk[i], tk[i], ch));
         if constexpr (kRowV) {
             static_assert(4 * VL == KL, "V rows in the K slots' registers");
 #pragma unroll
-            for (int i = 0; i < KL; ++i) vr[i] = __builtin_nontemporal_load(row_ptr(v_head, pk[i], tk[i], ch));
+            for (int i = 0; i < KL; ++i) vr[i] = ld(row_ptr(v_head, pk[i], tk[i], ch));
         } else {
 #pragma unroll
             for (int i = 0; i < VL; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t tok = min(key0 + 4 * (k0 + i * KSTEP) + j, last_tok);
-                    vr[4 * i + j] = __builtin_nontemporal_load(row_ptr(v_head, pv[i], tok, ch));
+                    vr[4 * i + j] = ld(row_ptr(v_head, pv[i], tok, ch));
                 }
         }
     }
@@ -1898,7 +1905,7 @@ constexpr size_t kVerifyTileLds = 2 * kVerifyTilesPerStep<D> * 2 * kTileBytes<D>
 // kAllTiles (D <= 128 only): each of the four consumer waves takes 32 query
 // vectors and both tiles of every step (up to 128 vectors per workgroup, one
 // record per partition), for calls with more than 64 vectors per KV head.
-template <int D, bool kAllTiles>
+template <int D, bool kAllTiles, bool kShared>
 __global__ __launch_bounds__(kVerifyThreads) __attribute__((amdgpu_waves_per_eu(2))) void
 attn_verify_kernel(const VerifyParams vp) {
     static_assert(!kAllTiles || D <= 128, "D = 256 splits the output dims instead");
@@ -1947,7 +1954,7 @@ attn_verify_kernel(const VerifyParams vp) {
         const uint32_t pt = tid - 256;                 // 0..255
         const uint32_t q = TPS == 2 ? pt >> 7 : 0u;    // which tile of the step
         const uint32_t gt0 = TPS == 2 ? pt & 127 : pt;
-        VerifyIo<D> io;
+        VerifyIo<D, kShared> io;
         io.lpt = p.log2_page_tokens;
         io.pt_mask = (1u << io.lpt) - 1;
         io.page_bytes = (D * 2) << io.lpt;
@@ -2186,17 +2193,17 @@ __global__ __launch_bounds__(64 * kCombineWaves) void attn_verify_combine_kernel
     if (!finite) atomicOr(p.err_word, kErrPrefillRange);
 }
 
-template <int D, bool kAllTiles>
+template <int D, bool kAllTiles, bool kShared = false>
 hipError_t launch_verify_d(hipStream_t stream, const VerifyParams &vp, uint32_t blocks,
                            uint32_t combine_rows) {
     const size_t lds = kVerifyTileLds<D> + kVerifyPageSlots * sizeof(int32_t);
     static_assert(kVerifyTileLds<D> + kVerifyPageSlots * sizeof(int32_t) <= 160 * 1024,
                   "verify LDS");
     static const hipError_t configured =
-        hipFuncSetAttribute((const void *)attn_verify_kernel<D, kAllTiles>,
+        hipFuncSetAttribute((const void *)attn_verify_kernel<D, kAllTiles, kShared>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (configured != hipSuccess) return configured;
-    SR_LAUNCH("attn_verify_kernel", (attn_verify_kernel<D, kAllTiles>), dim3(blocks),
+    SR_LAUNCH("attn_verify_kernel", (attn_verify_kernel<D, kAllTiles, kShared>), dim3(blocks),
               dim3(kVerifyThreads), lds, stream, vp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -2347,7 +2354,10 @@ hipError_t launch_attn_verify(hipStream_t stream, const AttnLaunch &a, const Seq
         return all_tiles ? launch_verify_d<128, true>(stream, vp, grid, waves)
                          : launch_verify_d<128, false>(stream, vp, grid, waves);
     }
-    return launch_verify_d<256, false>(stream, vp, grid, waves);
+    // several row slices read each partition's tiles: ordinary loads keep
+    // them in L2 for the sibling slices (D <= 128 calls fit one slice)
+    return vp.slices > 1 ? launch_verify_d<256, false, true>(stream, vp, grid, waves)
+                         : launch_verify_d<256, false>(stream, vp, grid, waves);
 }
 
 }  // namespace sr
