@@ -179,3 +179,84 @@ def test_generic_gdn_rollback_equals_oracle_and_reforward(pkg, backend, rng, dk,
         assert np.array_equal(h, fh)
         pool.close(f)
     pool.destroy()
+
+
+# ---------------------------------------------------------------------------
+# the generic path's own limits
+# ---------------------------------------------------------------------------
+
+def test_generic_width_more_rows_than_one_grid_holds(pkg, backend, rng, torch_mod):
+    # 66,000 rows of one sequence in one call: the generic kernels cover at
+    # most 65,535 rows per launch (grid y) and run the rest in a second
+    # launch, after every row's append.  Every V row is the same vector c, so
+    # each row's output is c whatever its softmax weights (sum p c / sum p).
+    torch = torch_mod
+    dim, rows = 4, 66000
+    pool = new_pool(pkg, backend, 1, dim, page_tokens=64, max_tokens=rows, seqs=1)
+    s = pool.open()
+    c = O.bf16_round(np.array([0.75, -1.5, 2.0, 0.125], np.float32))
+    q = torch.from_numpy(rng.standard_normal((rows, dim)).astype(np.float32)).cuda()
+    k = torch.from_numpy(rng.standard_normal((rows, dim)).astype(np.float32)).cuda()
+    v = torch.from_numpy(np.tile(c, (rows, 1))).cuda()
+    pos = torch.arange(rows, dtype=torch.int32, device="cuda").view(rows, 1).repeat(1, 3).contiguous()
+    out = torch.zeros((rows, dim), dtype=torch.float32, device="cuda")
+    pkg.attention_forward(backend, pool, [s], [rows], q, k, v, pos, out, heads=1, kv_heads=1,
+                          head_dim=dim, rotary_dim=dim, rope_theta=1e6)
+    got = out.cpu().numpy()
+    assert pool.len(s) == rows
+    # f32 sums over up to 66k weights: each row's sum p c / sum p keeps c to
+    # a few e-5 relative (recursive summation errs by at most rows * 2^-24);
+    # a row the second launch missed would read 0, a wrong V row another vector
+    err = np.abs(got - c[None, :])
+    assert err.max() <= 1e-3 * np.abs(c).max(), f"max abs {err.max():.3e} (row {err.max(1).argmax()})"
+    assert np.abs(got[65535:] - c).max() <= 1e-3 * np.abs(c).max()
+    # both launches appended: the first and the last rows read back as stored
+    kd, vd = pool.read(s, rows - 2, 2)
+    assert np.array_equal(vd, np.tile(c, (2, 1)))
+    pool.destroy()
+
+
+def test_generic_width_no_alloc_entry_point_equals_ordinary(pkg, backend, rng, torch_mod):
+    # the same generic-width call through both entry points, on forked copies
+    # of the same sequences: bit for bit
+    import ctypes as C
+    torch = torch_mod
+    dim, heads, kvh = 80, 4, 2
+    pool = new_pool(pkg, backend, kvh, dim, page_tokens=16, max_tokens=256, seqs=4)
+    a, b = pool.open(), pool.open()
+    ck = O.bf16_round(rng.standard_normal((30, kvh * dim)).astype(np.float32))
+    cv = O.bf16_round(rng.standard_normal((30, kvh * dim)).astype(np.float32))
+    pool.append(a, ck, cv)
+    fa, fb = pool.fork(a), pool.fork(b)
+    rows = [3, 20]
+    n = sum(rows)
+    q = torch.from_numpy(rng.standard_normal((n, heads * dim)).astype(np.float32)).cuda()
+    k = torch.from_numpy(rng.standard_normal((n, kvh * dim)).astype(np.float32)).cuda()
+    v = torch.from_numpy(rng.standard_normal((n, kvh * dim)).astype(np.float32)).cuda()
+    pos = torch.tensor([[30 + r] * 3 for r in range(3)] + [[r] * 3 for r in range(20)],
+                       dtype=torch.int32, device="cuda")
+    g = torch.from_numpy((1 + 0.02 * rng.standard_normal(dim)).astype(np.float32)).cuda()
+    outs = []
+    for seqs, entry in (([a, b], "safetyraise_kernel_attention_forward"),
+                        ([fa, fb], "safetyraise_kernel_attention_forward_noalloc")):
+        P = pkg.plugin
+        args = P.AttentionArgs()
+        args.struct_size = C.sizeof(P.AttentionArgs)
+        args.flags = P.DEVICE_POINTERS | P.QK_NORM | P.MROPE_INTERLEAVED
+        args.heads, args.kv_heads, args.head_dim, args.rotary_dim = heads, kvh, dim, dim
+        args.eps, args.rope_theta = 1e-6, 1e6
+        args.num_seqs = 2
+        ids = (C.c_uint32 * 2)(*seqs)
+        nr = (C.c_uint32 * 2)(*rows)
+        args.seq_ids, args.seq_rows = ids, nr
+        args.q, args.k, args.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+        args.q_norm = args.k_norm = g.data_ptr()
+        args.positions = pos.data_ptr()
+        out = torch.zeros((n, heads * dim), dtype=torch.float32, device="cuda")
+        args.out = out.data_ptr()
+        args.kv = pool.handle
+        backend.check(getattr(backend.lib, entry)(backend.context, C.byref(args)), entry)
+        outs.append(out.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    assert pool.len(a) == pool.len(fa) == 33 and pool.len(b) == pool.len(fb) == 20
+    pool.destroy()
