@@ -1322,6 +1322,63 @@ __device__ __forceinline__ void store_rows(const PrefillParams &p, uint32_t call
     if (!finite) atomicOr(p.err_word, kErrPrefillRange);
 }
 
+// store_rows for a wave's 32 rows through a 4 KB slice of LDS, 32 dims at a
+// time: the lanes write their accumulator values (row col, dims 8a + 4h ..)
+// to the slice and read them back row-major, so each store instruction
+// writes whole 128-byte lines (8 rows x 32 dims) instead of 32 bytes of each
+// of 32 rows.  Same values, gate and finite check as store_rows; rows from
+// `valid` on are not stored.
+template <int D>
+__device__ __forceinline__ void store_rows_lds(const PrefillParams &p, uint32_t call_row0,
+                                               int valid, uint32_t head, int h, int col,
+                                               int lane, float l_run,
+                                               const f32x16 (&oacc)[D / 32],
+                                               __attribute__((address_space(3))) f32x4 *slice) {
+    constexpr int NT = D / 32;
+    const bool bf16_in = (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) != 0;
+    const bool gated = (p.flags & SAFETYRAISE_MI355X_GATED) != 0;
+    const uint32_t hs = gated ? 2 * D : D;
+    const float inv_l = 1.0f / l_run;
+    bool finite = true;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            f32x4 o;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                o[bb] = oacc[tt][4 * a + bb] * inv_l;
+                finite = finite && (col >= valid || isfinite(o[bb]));
+            }
+            slice[col * 8 + ((2 * a + h) ^ (col & 7))] = o;
+        }
+        // LDS operations of one wave are performed in order; the fences keep
+        // the compiler from moving the reads above the writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * i + (lane >> 3), k = lane & 7;
+            f32x4 o = slice[r * 8 + (k ^ (r & 7))];
+            const uint32_t d0 = 32 * tt + 4 * k;
+            if (r < valid) {
+                const size_t row = (size_t)(call_row0 + r);
+                if (gated) {
+                    const size_t gbase = row * p.heads * hs + (size_t)head * hs + D + d0;
+#pragma unroll
+                    for (int bb = 0; bb < 4; ++bb) o[bb] *= ref_sigmoid(load_act(p.q, gbase + bb, bf16_in));
+                }
+                *(f32x4 *)(p.out + row * p.heads * D + (size_t)head * D + d0) = o;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (!finite) atomicOr(p.err_word, kErrPrefillRange);
+}
+
 // ---------------------------------------------------------------------------
 // attn_prefill_kernel: all waves of a workgroup process every tile in step
 // (one barrier per tile).  One workgroup = the G heads of a KV group x R
@@ -1442,6 +1499,11 @@ template <int D>
 constexpr uint32_t kRopePitch = D / 2 + 2;  // float2 per staged row
 template <int D, int G>
 constexpr size_t kRopeStageBytes = kStageRope<D, G> ? (size_t)2 * kRowTile * (4 / G) * kRopePitch<D> * 8 : 0;
+// the epilogue's 4 KB per wave (store_rows_lds), in the same area: the
+// RoPE rows are read only in the prologue
+constexpr size_t kOutStageBytes = 8 * 4096;
+template <int D, int G>
+constexpr size_t kPpExtraLds = kRopeStageBytes<D, G> > kOutStageBytes ? kRopeStageBytes<D, G> : kOutStageBytes;
 
 template <int D, int G, bool kTilePage>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2))) void
@@ -1644,9 +1706,10 @@ attn_prefill_pp_kernel(const PrefillParams p) {
     pv_tile_rows<D>(vbuf + ((n - 1) & 1) * kTileBytes<D>, voff, pop, oacc);
     if (grp == 0) __syncthreads();  // matches group 1's extra barrier
 
-    const uint32_t row = wrow0 + col;
     const float l = xhalf_sum(l_run);
-    if (row < b.m.rows) store_rows<D>(p, b.m.row0 + row, head, qbase, h, l, oacc);
+    const int valid = min((int)b.m.rows - (int)wrow0, kRowTile);
+    store_rows_lds<D>(p, b.m.row0 + wrow0, valid, head, h, col, lane, l, oacc,
+                      (__attribute__((address_space(3))) f32x4 *)(lds + kPingPongLds<D>) + wave * 256);
 }
 
 template <int D, int G>
@@ -1662,7 +1725,7 @@ hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t bloc
     // the LDS limits are raised once per instantiation (thread-safe static
     // initialisers): both kernels take more than the default
     if constexpr (kUsePingPong<D, G>) {
-        const size_t lds = kPingPongLds<D> + kRopeStageBytes<D, G>;
+        const size_t lds = kPingPongLds<D> + kPpExtraLds<D, G>;
         static const hipError_t configured =
             hipFuncSetAttribute((const void *)attn_prefill_pp_kernel<D, G, kTilePage>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
