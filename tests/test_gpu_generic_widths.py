@@ -260,3 +260,42 @@ def test_generic_width_no_alloc_entry_point_equals_ordinary(pkg, backend, rng, t
     assert np.array_equal(outs[0], outs[1])
     assert pool.len(a) == pool.len(fa) == 33 and pool.len(b) == pool.len(fb) == 20
     pool.destroy()
+
+
+def test_generic_width_more_sequences_than_one_launch_holds(pkg, backend, rng):
+    # 70 sequences in one call: the generic kernels take 64 sequences per
+    # launch (their argument block), so the call runs as two launch pairs
+    dim = 40
+    pool = new_pool(pkg, backend, 1, dim, page_tokens=16, max_tokens=64, seqs=70)
+    ctxs = [int(rng.integers(0, 20)) for _ in range(70)]
+    cases = [Case(rng, pool, 3, 1, dim, ctx=ctx, rows=1 + (i % 3), max_tokens=64)
+             for i, ctx in enumerate(ctxs)]
+    run_case(pkg, backend, pool, cases, rotary=dim)
+    for c, ctx in zip(cases, ctxs):
+        assert pool.len(c.seq) == ctx + c.rows
+    pool.destroy()
+
+
+def test_generic_gdn_more_sequences_than_one_launch_holds(pkg, backend, rng):
+    # 70 sequences of one decode row each at key width 64 (the generic GDN
+    # kernel), from distinct seeded states
+    L = Layer(rng, 1, 2, 64, 48, 4)
+    n = 70
+    pool = pkg.GdnState(backend, 1, 2, 64, 48, 4, n)
+    seqs, states = [], []
+    for _ in range(n):
+        s = pool.open()
+        m = (0.05 * rng.standard_normal((2, 48, 64))).astype(np.float32)
+        h = (0.5 * rng.standard_normal((L.C, 3))).astype(np.float32)
+        pool.write(s, m, h)
+        seqs.append(s)
+        states.append((m, h))
+    xs = [L.inputs(rng, 1) for _ in range(n)]
+    x = tuple(np.concatenate([u[i] for u in xs]) for i in range(4))
+    got = plugin_rows(pkg, backend, pool, L, seqs, [1] * n, x)
+    for i, (m, h) in enumerate(states):
+        gdn_close(got[i:i + 1], oracle_rows(L, xs[i], m, h), what=f"sequence {i}")
+        gm, gh = pool.read(seqs[i])
+        gdn_close(gm, m, what=f"state {i}")
+        assert np.array_equal(gh, h), f"history {i}"
+    pool.destroy()
