@@ -1712,18 +1712,446 @@ attn_prefill_pp_kernel(const PrefillParams p) {
                       (__attribute__((address_space(3))) f32x4 *)(lds + kPingPongLds<D>) + wave * 256);
 }
 
+// softmax_tile_ref in parts, so that a caller can issue the common part
+// between MFMAs of its own: softmax_mask1 (the causal mask of a diagonal
+// tile), softmax_probs1 (p = 2^(s - shift) in fp16 and the lane's sum of
+// those values) and softmax_fixup1 (the wave-uniform ballot and the rare
+// branch that moves the reference maximum).
+template <bool kMasked>
+__device__ __forceinline__ void softmax_mask1(f32x16 (&sacc)[2], uint32_t key0,
+                                              uint32_t key_limit, int h) {
+    if constexpr (kMasked) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t key = key0 + 32 * kb + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (key > key_limit) sacc[kb][i] = -INFINITY;
+            }
+    }
+}
+// p = 2^(sacc - shift) in fp16 (k-step st's 8 values packed in pop[st]), and
+// the lane's sum of those values
+__device__ __forceinline__ float softmax_probs1(const f32x16 (&sacc)[2], float shift,
+                                                u32x4 (&pop)[4]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        f32x8 v;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = fast_exp2(sacc[st >> 1][8 * (st & 1) + j] - shift);
+        pop[st] = __builtin_bit_cast(u32x4, __builtin_convertvector(v, f16x8));
+    }
+    return (sum_f16x8(__builtin_bit_cast(f16x8, pop[0]), 0.0f) +
+            sum_f16x8(__builtin_bit_cast(f16x8, pop[1]), 0.0f)) +
+           (sum_f16x8(__builtin_bit_cast(f16x8, pop[2]), 0.0f) +
+            sum_f16x8(__builtin_bit_cast(f16x8, pop[3]), 0.0f));
+}
+// the rare branch of softmax_tile_ref: taken on the first tile and when a
+// lane's partial sum exceeds kPSumMax
+template <int D>
+__device__ __forceinline__ void softmax_fixup1(const f32x16 (&sacc)[2], bool first, float lt,
+                                               float &m_run, f32x16 &negm, float &l_run,
+                                               f32x16 (&oacc)[D / 32], u32x4 (&pop)[4]) {
+    constexpr int NT = D / 32;
+    if (__builtin_amdgcn_ballot_w64(first || !(lt <= kPSumMax)) != 0) {
+        asm volatile("; softmax reference maximum moves" ::: "memory");
+        float m11[11];
+#pragma unroll
+        for (int j = 0; j < 10; ++j) {
+            const int e = 3 * j;
+            m11[j] = max3_raw(sacc[e >> 4][e & 15], sacc[(e + 1) >> 4][(e + 1) & 15],
+                              sacc[(e + 2) >> 4][(e + 2) & 15]);
+        }
+        m11[10] = max3_raw(sacc[1][14], sacc[1][15], sacc[1][15]);
+        const float m4a = max3_raw(m11[0], m11[1], m11[2]);
+        const float m4b = max3_raw(m11[3], m11[4], m11[5]);
+        const float m4c = max3_raw(m11[6], m11[7], m11[8]);
+        const float m4d = max3_raw(m11[9], m11[10], m11[10]);
+        const float mx = xhalf_max(max3_raw(max3_raw(m4a, m4b, m4c), m4d, m4d));
+        // a row whose scores here are all masked has mx = -inf: no shift
+        const float shift = first ? mx : fmaxf(mx, 0.0f);
+        m_run += shift;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negm[i] = -m_run;
+        // (l and O are still 0 on the first tile, whose shift may be any size)
+        const float alpha = first ? 1.0f : fast_exp2(-shift);
+        l_run *= alpha;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[tt][i] *= alpha;
+        lt = softmax_probs1(sacc, shift, pop);
+    }
+    l_run += lt;
+}
+
+// ---------------------------------------------------------------------------
+// attn_prefill_pipe_kernel (D = 128, G = 2, 4 or 8, page_tokens >= 64): 8
+// waves, two per SIMD, each one unit of (query head, 32 rows); G heads x
+// 8/G row blocks per workgroup.  Every wave overlaps its own MFMAs with its
+// own vector work, software-pipelined over the tiles, with one barrier per
+// tile:
+//
+//   step t   S(t) = K(t) Q^T              convert + store a share of K(t+1)
+//                                           and V(t); load its share of
+//                                           K(t+2) and V(t+1)
+//            O += V(t-1) P(t-1)           softmax(t) -> P(t)
+//            barrier
+//
+// Each chunk between two sched_barriers is one MFMA and the vector work
+// issued in its shadow: three VALU of the staging after each S MFMA, one
+// pair of probabilities (two exps, a pack, a dot2 into the row sum) after
+// each P V MFMA.  The two waves of a SIMD interleave at the hardware's
+// choice.  All MFMAs keep their accumulators in VGPRs (at most 256
+// registers per wave): an MFMA with AGPR accumulators holds its wave's
+// issue about twice as long.
+//
+// K(t) lives in K buffer t & 1 and V(t) in V buffer t & 1: step t writes K
+// buffer (t+1) & 1, last read by S(t-1), and V buffer t & 1, last read by
+// the P V product of step t-1, both before the previous barrier.  P is
+// double-buffered in registers; a rescale of O (the softmax's rare branch)
+// comes after the step's P V product.
+//
+// LDS images, fp16, read with 16-byte loads only: K rows of 128 dims at a
+// pitch of 272 bytes, V^T rows (one per dim, 64 keys in the column order of
+// the S^T accumulator, as TileIo::store_v) at 144 bytes.  The pitches put the
+// 16 lanes of a read, which hit 16 consecutive rows, on 16 distinct 4-bank
+// groups, so every operand address is one base register plus an immediate.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPipeKPitch = 272;
+constexpr uint32_t kPipeVPitch = 144;
+constexpr uint32_t kPipeKTile = kKeyTile * kPipeKPitch;  // 17408
+constexpr uint32_t kPipeVTile = 128 * kPipeVPitch;       // 18432
+constexpr uint32_t kPipeV0 = 2 * kPipeKTile;
+constexpr uint32_t kPipeX0 = kPipeV0 + 2 * kPipeVTile;   // RoPE rows, then output slices
+template <int G>
+constexpr int kPipeRowBlocks = 8 / G;
+template <int G>
+constexpr uint32_t kPipeRopeBytes = (uint32_t)kRowTile * kPipeRowBlocks<G> * kRopePitch<128> * 8;
+template <int G>
+constexpr uint32_t kPipeLds = kPipeX0 + (kPipeRopeBytes<G> > 8 * 4096 ? kPipeRopeBytes<G> : 8 * 4096);
+
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+
+template <int G>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+attn_prefill_pipe_kernel(const PrefillParams p) {
+    constexpr int D = 128;
+    constexpr int RB = kPipeRowBlocks<G>;
+    constexpr int NT = D / 32;
+    constexpr int NS = D / 16;
+    static_assert(G == 2 || G == 4 || G == 8, "pipe kernel group sizes");
+    static_assert(kPipeLds<G> <= 160 * 1024, "LDS");
+    extern __shared__ __align__(16) unsigned char lds[];
+    auto lds_at = [&](uint32_t off) __attribute__((always_inline)) {
+        return (__attribute__((address_space(3))) unsigned char *)(lds) + off;
+    };
+
+    const int tid = threadIdx.x;
+    const int wave = wave_index();
+    const int lane = tid & 63;
+    const int h = lane >> 5;
+    const int col = lane & 31;
+    const QArgs qa = q_args(p);
+    const BlockPos b = block_pos(p, kRowTile * RB);
+    if (!b.active) return;
+    const uint32_t head = b.kvh * G + (wave % G);
+    const uint32_t wrow0 = b.row0 + kRowTile * (wave / G);
+    const uint32_t my_row = min(wrow0 + col, b.m.rows - 1);
+    const uint32_t key_limit = b.m.ctx + my_row;
+    const uint32_t first_row_limit = b.m.ctx + b.row0;
+    const uint32_t hs = (p.flags & SAFETYRAISE_MI355X_GATED) ? 2 * D : D;
+    const size_t qbase = (size_t)(b.m.row0 + my_row) * p.heads * hs + (size_t)head * hs;
+    const uint32_t n = b.n_tiles;
+
+    // tile t of the sequence: one page (page_tokens >= 64), wave-uniform
+    const int32_t *table = p.page_table + (size_t)b.m.slot * p.pages_per_seq;
+    const size_t head_base = (size_t)(b.kvh / p.kv_rep) * p.num_pages;
+    const uint32_t lpt = p.log2_page_tokens;
+    const uint32_t pt_mask = (1u << lpt) - 1;
+    auto page_of = [&](uint32_t t) __attribute__((always_inline)) {
+        return (uint32_t)table[(min(t, n - 1) * kKeyTile) >> lpt];
+    };
+    auto tile_ptr = [&](const uint16_t *src, uint32_t t, uint32_t pg) __attribute__((always_inline)) {
+        const uint32_t tc = min(t, n - 1);
+        uint64_t tp = (uint64_t)(src + (((head_base + __builtin_amdgcn_readfirstlane(pg)) << lpt) +
+                                        ((tc * kKeyTile) & pt_mask)) * D);
+        pin_s(tp);
+        return global_from_bits<const unsigned char>(tp);
+    };
+    // Per-thread offsets, recomputed where used from a lane id read with
+    // mbcnt in a volatile asm (not hoisted or merged), so that none of them is
+    // live across the q prologue's register peak.
+    //   staging (512 threads): K rows 2 r, 2 r + 1 (r = tid / 16), 16-byte
+    //   chunk tid % 16 of each; V keys 4 g .. 4 g + 3 (g = tid % 16), dims
+    //   4 c .. 4 c + 3 (c = tid / 16), as 8-byte pieces
+    //   operand reads: K row col (+32 for the second key half), V^T row col
+    //   (+32 per dim tile); k-step st adds 32 bytes
+    struct Offs {
+        uint32_t k_goff, v_goff, k_loff, v_loff, kr, vr;
+    };
+    auto offs = [&]() __attribute__((always_inline)) {
+        uint32_t l;
+        asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+        const uint32_t lo = l & 15, hi = (uint32_t)wave * 4 + (l >> 4);
+        const uint32_t c = l & 31, hh = l >> 5;
+        Offs o;
+        o.k_goff = hi * 2 * (D * 2) + lo * 16;
+        o.v_goff = lo * 4 * (D * 2) + hi * 8;
+        o.k_loff = hi * 2 * kPipeKPitch + lo * 16;
+        o.v_loff = hi * 4 * kPipeVPitch + 32 * (lo >> 2) + 16 * (lo & 1) + 8 * ((lo >> 1) & 1);
+        o.kr = c * kPipeKPitch + hh * 16;
+        o.vr = c * kPipeVPitch + hh * 16;
+        return o;
+    };
+    const uint32_t vg = tid & 15;  // the thread's V key group (masking)
+    auto load_k = [&](u32x4 (&r)[2], const unsigned char *tile, uint32_t goff)
+                      __attribute__((always_inline)) {
+        uint32_t o = goff;
+        pin(o);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) r[i] = *(const u32x4 *)(tile + o + i * (D * 2));
+    };
+    auto load_v = [&](u32x2 (&r)[4], const unsigned char *tile, uint32_t goff)
+                      __attribute__((always_inline)) {
+        uint32_t o = goff;
+        pin(o);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[j] = *(const u32x2 *)(tile + o + j * (D * 2));
+    };
+
+    u32x4 sk[2];  // K(t+1) at the start of step t
+    u32x2 sv[4];  // V(t)
+    f16x8 qop[NS];
+    {
+        u32x4 s0[2];
+        const uint32_t pg0 = page_of(0), pg1 = page_of(1);
+        const Offs o0 = offs();
+        load_k(s0, tile_ptr(p.k_pages, 0, pg0), o0.k_goff);
+        load_k(sk, tile_ptr(p.k_pages, 1, pg1), o0.k_goff);
+        load_v(sv, tile_ptr(p.v_pages, 0, pg0), o0.v_goff);
+        // RoPE (cos, sin) rows of the workgroup in LDS for the q prologue
+        // (every load issued before any store)
+        typedef __attribute__((address_space(3))) float2 lds_float2;
+        lds_float2 *rs = (lds_float2 *)lds_at(kPipeX0);
+        constexpr uint32_t kRows = kRowTile * RB;
+        constexpr uint32_t kChunks = kRows * (D / 4);
+        constexpr uint32_t kPer = kChunks / 512;
+        static_assert(kChunks % 512 == 0, "chunks per thread");
+        const uint32_t cpr = qa.rotary_dim / 4;
+        f32x4 cv[kPer];
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = min((uint32_t)tid + 512 * u, kRows * cpr - 1);
+            const uint32_t rr = c / cpr, k = c - rr * cpr;
+            const uint32_t call_row = b.m.row0 + min(b.row0 + rr, b.m.rows - 1);
+            cv[u] = *(const f32x4 *)(qa.rope_cs + (size_t)call_row * (qa.rotary_dim / 2) + 2 * k);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kPer; ++u) {
+            const uint32_t c = tid + 512 * u;
+            if (c < kRows * cpr) {
+                const uint32_t rr = c / cpr, k = c - rr * cpr;
+                *(__attribute__((address_space(3))) f32x4 *)(rs + rr * kRopePitch<D> + 2 * k) = cv[u];
+            }
+        }
+        __syncthreads();
+        const LdsRope rope{rs + (my_row - b.row0) * kRopePitch<D>};
+        q_operands<D>(qa, qbase, b.m.row0 + my_row, h, lane, qop, &rope);
+        const Offs o1 = offs();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            u32x4 f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f[j] = pack_f16x2(bf16lo(s0[i][j]), bf16hi(s0[i][j]));
+            *(lds_u32x4 *)lds_at(o1.k_loff + i * kPipeKPitch) = f;
+        }
+        __syncthreads();
+    }
+
+    f32x16 oacc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+    float m_run = 0.0f, l_run = 0.0f;
+    f32x16 negm = {};  // -m_run in every element: the S accumulators' start
+    u32x4 popA[4], popB[4];
+    uint32_t pg_k = page_of(2), pg_v = page_of(1);  // K(t+2) and V(t+1), loaded in step t
+
+    auto step = [&](uint32_t t, auto par, auto masked, auto has_pv, u32x4 (&pprev)[4],
+                    u32x4 (&pcur)[4]) __attribute__((always_inline)) {
+        constexpr uint32_t PAR = decltype(par)::value;
+        constexpr bool MASKED = decltype(masked)::value;
+        constexpr bool HAS_PV = decltype(has_pv)::value;
+        const uint32_t pgk = pg_k, pgv = pg_v;
+        pg_v = pg_k;
+        pg_k = page_of(t + 3);
+        const Offs o = offs();
+        const uint32_t kbase = PAR * kPipeKTile + o.kr;
+        const uint32_t kdst = (PAR ^ 1) * kPipeKTile + o.k_loff;
+        const uint32_t vdst = kPipeV0 + PAR * kPipeVTile + o.v_loff;
+        const uint32_t valid = MASKED ? min((uint32_t)kKeyTile, b.n_keys - t * kKeyTile)
+                                      : (uint32_t)kKeyTile;
+        // staging job j (three VALU): j < 8 converts K word j & 3 of row
+        // j / 4 and stores the row's chunk after its last word; j >= 8
+        // converts the low (keys 4 g, 4 g + 1) or high pair of V^T dim
+        // 4 c + (j - 8) / 2 and stores the dim's piece after its high pair;
+        // a register set is refilled right after its last conversion
+        u32x4 kw;
+        uint32_t vlo = 0;
+        auto stage_job = [&](int j) __attribute__((always_inline)) {
+            if (j < 8) {
+                const int i = j >> 2, w = j & 3;
+                kw[w] = pack_f16x2(bf16lo(sk[i][w]), bf16hi(sk[i][w]));
+                if (w == 3) *(lds_u32x4 *)lds_at(kdst + i * kPipeKPitch) = kw;
+                if (j == 7) load_k(sk, tile_ptr(p.k_pages, t + 2, pgk), o.k_goff);
+            } else {
+                const int jj = j - 8, e = jj >> 1, hi = jj & 1;
+                if (MASKED && jj == 0) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (4 * vg + q >= valid) sv[q] = u32x2{0, 0};
+                }
+                const uint32_t w0 = sv[2 * hi][e >> 1], w1 = sv[2 * hi + 1][e >> 1];
+                const uint32_t pr = (e & 1) ? pack_f16x2(bf16hi(w0), bf16hi(w1))
+                                            : pack_f16x2(bf16lo(w0), bf16lo(w1));
+                if (!hi) {
+                    vlo = pr;
+                } else {
+                    *(lds_u32x2 *)lds_at(vdst + e * kPipeVPitch) = u32x2{vlo, pr};
+                }
+                if (j == 15) load_v(sv, tile_ptr(p.v_pages, t + 1, pgv), o.v_goff);
+            }
+        };
+        f16x8 kf[NS][2];
+        auto read_k = [&](int st) __attribute__((always_inline)) {
+            kf[st][0] = *(const lds_f16x8 *)lds_at(kbase + st * 32);
+            kf[st][1] = *(const lds_f16x8 *)lds_at(kbase + 32 * kPipeKPitch + st * 32);
+        };
+        f32x16 sacc[2];
+        read_k(0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            if (st + 1 < NS) read_k(st + 1);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st][kb], qop[st],
+                                                                  st ? sacc[kb] : negm, 0, 0, 0);
+                stage_job(2 * st + kb);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        softmax_mask1<MASKED>(sacc, t * kKeyTile, key_limit, h);
+        // probability job j: the pair j & 3 of k-step j / 4
+        float ls[4] = {};
+        auto prob_job = [&](int j) __attribute__((always_inline)) {
+            const int st = j >> 2, pr = j & 3;
+            const int e = 8 * (st & 1) + 2 * pr;
+            const uint32_t w = pack_f16x2(fast_exp2(sacc[st >> 1][e]), fast_exp2(sacc[st >> 1][e + 1]));
+            pcur[st][pr] = w;
+            const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+            ls[st] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, ls[st], false);
+        };
+        if constexpr (HAS_PV) {
+            const uint32_t vbase = kPipeV0 + (PAR ^ 1) * kPipeVTile + o.vr;
+            auto vfrag = [&](int i) __attribute__((always_inline)) {
+                const int st = i >> 2, tt = i & 3;
+                return *(const lds_f16x8 *)lds_at(vbase + tt * 32 * kPipeVPitch + st * 32);
+            };
+            f16x8 va = vfrag(0);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int st = i >> 2, tt = i & 3;
+                const f16x8 a = va;
+                if (i + 1 < 16) va = vfrag(i + 1);
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    a, __builtin_bit_cast(f16x8, pprev[st]), oacc[tt], 0, 0, 0);
+                prob_job(i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) prob_job(j);
+        }
+        const float lt = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+        softmax_fixup1<D>(sacc, t == 0, lt, m_run, negm, l_run, oacc, pcur);
+        __syncthreads();
+    };
+    auto pv_last = [&](uint32_t vbuf, const u32x4 (&pop)[4]) __attribute__((always_inline)) {
+        const uint32_t vbase = vbuf + offs().vr;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int tt = 0; tt < NT; ++tt) {
+                const f16x8 a = *(const lds_f16x8 *)lds_at(vbase + tt * 32 * kPipeVPitch + st * 32);
+                oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    a, __builtin_bit_cast(f16x8, pop[st]), oacc[tt], 0, 0, 0);
+            }
+        }
+    };
+    using Even = std::integral_constant<uint32_t, 0>;
+    using Odd = std::integral_constant<uint32_t, 1>;
+    using Whole = std::false_type;
+    using Masked = std::true_type;
+    using NoPv = std::false_type;
+    using Pv = std::true_type;
+    // steps t < t_main: every row sees all of tile t, and V(t) is whole
+    const uint32_t t_main = min((first_row_limit + 1) / kKeyTile, n - 1);
+    if (t_main > 0) step(0, Even{}, Whole{}, NoPv{}, popB, popA);
+    else step(0, Even{}, Masked{}, NoPv{}, popB, popA);
+    uint32_t t = 1;
+    for (; t + 1 < t_main; t += 2) {
+        step(t, Odd{}, Whole{}, Pv{}, popA, popB);
+        step(t + 1, Even{}, Whole{}, Pv{}, popB, popA);
+    }
+    for (; t + 1 < n; t += 2) {
+        step(t, Odd{}, Masked{}, Pv{}, popA, popB);
+        step(t + 1, Even{}, Masked{}, Pv{}, popB, popA);
+    }
+    if (t < n) {
+        step(t, Odd{}, Masked{}, Pv{}, popA, popB);
+        pv_last(kPipeV0 + kPipeVTile, popB);
+    } else {
+        pv_last(kPipeV0, popA);
+    }
+
+    // the output slices share the RoPE rows' area, read only in the prologue
+    const int valid = min((int)b.m.rows - (int)wrow0, kRowTile);
+    store_rows_lds<D>(p, b.m.row0 + wrow0, valid, head, h, col, lane, xhalf_sum(l_run), oacc,
+                      (__attribute__((address_space(3))) f32x4 *)lds_at(kPipeX0) + wave * 256);
+}
+
 template <int D, int G>
 constexpr bool kUsePingPong = (D == 128) && (G == 1 || G == 2 || G == 4);
 
+// the pipelined kernel takes D = 128 at G = 2, 4 or 8 with tiles inside one
+// page; the ping-pong kernel the other D = 128 cases with G = 1, 2 or 4;
+// the lock-step kernel the rest
 template <int D, int G>
-uint32_t rows_per_block_dg() {
+constexpr bool kHasPipe = (D == 128) && (G == 2 || G == 4 || G == 8);
+
+template <int D, int G>
+bool use_pipe(const PrefillParams &p) {
+    if constexpr (kHasPipe<D, G>) return p.log2_page_tokens >= 6;
+    return false;
+}
+
+template <int D, int G>
+uint32_t rows_per_block_dg(bool pipe) {
+    if constexpr (kHasPipe<D, G>) {
+        if (pipe) return kRowTile * kPipeRowBlocks<G>;
+    }
     return kUsePingPong<D, G> ? 2 * kRowTile * (4 / G) : kRowTile * kLockstepRows<G>;
 }
 
 template <int D, int G, bool kTilePage>
 hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t blocks) {
     // the LDS limits are raised once per instantiation (thread-safe static
-    // initialisers): both kernels take more than the default
+    // initialisers): the kernels take more than the default
     if constexpr (kUsePingPong<D, G>) {
         const size_t lds = kPingPongLds<D> + kPpExtraLds<D, G>;
         static const hipError_t configured =
@@ -1744,9 +2172,21 @@ hipError_t launch_attn(hipStream_t stream, const PrefillParams &p, uint32_t bloc
     return hipGetLastError();
 }
 
+template <int G>
+hipError_t launch_pipe(hipStream_t stream, const PrefillParams &p, uint32_t blocks) {
+    static const hipError_t configured =
+        hipFuncSetAttribute((const void *)attn_prefill_pipe_kernel<G>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPipeLds<G>);
+    if (configured != hipSuccess) return configured;
+    SR_LAUNCH("attn_prefill_pipe_kernel", (attn_prefill_pipe_kernel<G>), dim3(blocks), dim3(512),
+              kPipeLds<G>, stream, p);
+    return hipGetLastError();
+}
+
 template <int D, int G>
 hipError_t launch_dg(hipStream_t stream, PrefillParams &p, const SeqMeta *seqs, int nseq) {
-    const uint32_t rpb = rows_per_block_dg<D, G>();
+    const bool pipe = use_pipe<D, G>(p);
+    const uint32_t rpb = rows_per_block_dg<D, G>(pipe);
     uint32_t max_blk = 0, max_rows = 0;
     for (int i = 0; i < nseq; ++i) {
         PrefillMeta &m = p.meta[i];
@@ -1763,6 +2203,9 @@ hipError_t launch_dg(hipStream_t stream, PrefillParams &p, const SeqMeta *seqs, 
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t blocks = p.max_blk * p.nseq * p.kv_heads;
+    if constexpr (kHasPipe<D, G>) {
+        if (pipe) return launch_pipe<G>(stream, p, blocks);
+    }
     if (p.log2_page_tokens >= 6) return launch_attn<D, G, true>(stream, p, blocks);
     return launch_attn<D, G, false>(stream, p, blocks);
 }

@@ -5,10 +5,12 @@ every key whose score beats it, rescales the running sum and output by
 e^(m - m') before adding the key (src/model/math.rs:133-152).  The MI355X
 kernels move their maximum less often:
 
-* the ping-pong prefill kernel (G = 1, 2, 4 at head_dim 128) keeps the row
-  maximum of its first 64-key tile and raises it only when a lane's partial
-  sum of a tile's probabilities exceeds 2^15 (a score about 15 log2 units
-  above the kept maximum, or many keys a little lower);
+* the pipelined prefill kernel (G = 2, 4, 8 at head_dim 128, pages of 64
+  tokens or more) and the ping-pong prefill kernel (G = 1, and G = 2, 4 on
+  smaller pages) keep the row maximum of their first 64-key tile and raise
+  it only when a lane's partial sum of a tile's probabilities exceeds 2^15 (a
+  score about 15 log2 units above the kept maximum, or many keys a little
+  lower);
 * the lock-step prefill kernel (other group sizes and head dims) and the
   verify kernel raise it when a tile's maximum is more than 8 log2 units
   above it;
@@ -184,34 +186,39 @@ def falling_plants(rows, heads, gaps):
 
 
 PP = ("attn_prefill_pp_kernel",)
+PIPE = ("attn_prefill_pipe_kernel",)
 LOCKSTEP = ("attn_prefill_kernel",)
 NOT_DECODE = ("attn_decode_kernel",)
 
 
 # ---------------------------------------------------------------------------
-# prefill: the ping-pong kernel (G = 1, 2, 4; head_dim 128)
+# prefill: the pipelined kernel (G = 2, 4, 8; head_dim 128; pages >= 64) and
+# the ping-pong kernel (G = 1; G = 2, 4 on 16-token pages)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("heads,kv_heads", [(32, 8), (8, 8), (16, 8)])
-def test_pingpong_prefill_rising_maxima(pkg, backend, rng, heads, kv_heads):
+@pytest.mark.parametrize("heads,kv_heads,page,kernel", [(32, 8, 64, PIPE), (8, 8, 64, PP),
+                                                        (16, 8, 64, PIPE), (64, 8, 64, PIPE),
+                                                        (32, 8, 16, PP)])
+def test_prefill_rising_maxima(pkg, backend, rng, heads, kv_heads, page, kernel):
     # every row's maximum rises three times after the first tile: +10, +20
     # and +40 log2 units over its first-tile maximum
-    pool = new_pool(pkg, backend, kv_heads, 128, max_tokens=1024, seqs=1)
+    pool = new_pool(pkg, backend, kv_heads, 128, page_tokens=page, max_tokens=1024, seqs=1)
     gq, gk = gammas(rng, 128)
     rows = 128
     plants = rising_plants(rows, heads, (64, 256, 448), (10.0, 20.0, 40.0))
     s = PlantedSeq(rng, pool, heads, kv_heads, 128, 640, rows, plants, gq=gq)
-    run_planted(pkg, backend, pool, [s], gq=gq, gk=gk, expect=PP, forbid=NOT_DECODE)
+    run_planted(pkg, backend, pool, [s], gq=gq, gk=gk, expect=kernel, forbid=NOT_DECODE)
     pool.destroy()
 
 
-def test_pingpong_prefill_thresholds_dense_tile_and_falls(pkg, backend, rng):
+@pytest.mark.parametrize("page,kernel", [(64, PIPE), (16, PP)])
+def test_prefill_thresholds_dense_tile_and_falls(pkg, backend, rng, page, kernel):
     # one call, three sequences at G = 4: single plants across the lazy and
     # fp16-sum thresholds, a whole tile of equal planted scores (sum 2^16
     # with every p finite), and first-tile plants 12 and 40 log2 units above
     # every later key
     heads, kv_heads, dim = 32, 8, 128
-    pool = new_pool(pkg, backend, kv_heads, dim, max_tokens=1024, seqs=3)
+    pool = new_pool(pkg, backend, kv_heads, dim, page_tokens=page, max_tokens=1024, seqs=3)
     gq, gk = gammas(rng, dim)
     gaps = (5.0, 7.9, 8.1, 12.0, 14.9, 15.1, 15.9, 16.1, 17.0, 30.0)
     a = PlantedSeq(rng, pool, heads, kv_heads, dim, 400, 96,
@@ -220,17 +227,22 @@ def test_pingpong_prefill_thresholds_dense_tile_and_falls(pkg, backend, rng):
                    dense_tile_plants(heads, kv_heads, 128, 10.0, 64), gq=gq)
     c = PlantedSeq(rng, pool, heads, kv_heads, dim, 500, 80,
                    falling_plants(80, heads, (12.0, 40.0)), gq=gq)
-    run_planted(pkg, backend, pool, [a, b, c], gq=gq, gk=gk, expect=PP, forbid=NOT_DECODE)
+    run_planted(pkg, backend, pool, [a, b, c], gq=gq, gk=gk, expect=kernel, forbid=NOT_DECODE)
     pool.destroy()
 
 
 # ---------------------------------------------------------------------------
-# prefill: the lock-step kernel (G = 3, 5, 7, > 8; head_dim 64 and 256)
+# prefill: the lock-step kernel (G = 3, 5, 7; head_dim 64 and 256), and a
+# group of 16 heads (run as two groups of 8 on the pipelined kernel)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("heads,kv_heads,dim", [(12, 4, 128), (10, 2, 128), (32, 2, 128),
-                                                (14, 2, 64), (8, 2, 256)])
-def test_lockstep_prefill_rising_thresholds_and_falls(pkg, backend, rng, heads, kv_heads, dim):
+@pytest.mark.parametrize("heads,kv_heads,dim,kernel", [(12, 4, 128, LOCKSTEP),
+                                                       (10, 2, 128, LOCKSTEP),
+                                                       (32, 2, 128, PIPE),
+                                                       (14, 2, 64, LOCKSTEP),
+                                                       (8, 2, 256, LOCKSTEP)])
+def test_lockstep_prefill_rising_thresholds_and_falls(pkg, backend, rng, heads, kv_heads, dim,
+                                                      kernel):
     pool = new_pool(pkg, backend, kv_heads, dim, max_tokens=1024, seqs=3)
     gq, gk = gammas(rng, dim)
     a = PlantedSeq(rng, pool, heads, kv_heads, dim, 640, 96,
@@ -242,8 +254,7 @@ def test_lockstep_prefill_rising_thresholds_and_falls(pkg, backend, rng, heads, 
                       for r in range(40)], gq=gq)
     c = PlantedSeq(rng, pool, heads, kv_heads, dim, 200, 48,
                    falling_plants(48, heads, (12.0, 40.0)), gq=gq)
-    run_planted(pkg, backend, pool, [a, b, c], gq=gq, gk=gk, expect=LOCKSTEP,
-                forbid=NOT_DECODE)
+    run_planted(pkg, backend, pool, [a, b, c], gq=gq, gk=gk, expect=kernel, forbid=NOT_DECODE)
     pool.destroy()
 
 
@@ -320,5 +331,5 @@ def test_qwen3_8b_prefill_last_chunk_at_context_3584(pkg, backend, rng):
         s.q = O.bf16_round(s.q)
         s.k = O.bf16_round(s.k)
         s.v = O.bf16_round(s.v)
-    run_planted(pkg, backend, pool, seqs, gq=gq, gk=gk, expect=PP, forbid=NOT_DECODE)
+    run_planted(pkg, backend, pool, seqs, gq=gq, gk=gk, expect=PIPE, forbid=NOT_DECODE)
     pool.destroy()
