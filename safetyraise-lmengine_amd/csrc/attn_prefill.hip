@@ -1979,6 +1979,7 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
     f32x16 negm = {};  // -m_run in every element: the S accumulators' start
     u32x4 popA[4], popB[4];
     uint32_t pg_k = page_of(2), pg_v = page_of(1);  // K(t+2) and V(t+1), loaded in step t
+    const Offs o = offs();  // (after the prologue's register peak)
 
     auto step = [&](uint32_t t, auto par, auto masked, auto has_pv, u32x4 (&pprev)[4],
                     u32x4 (&pcur)[4]) __attribute__((always_inline)) {
@@ -1988,7 +1989,6 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
         const uint32_t pgk = pg_k, pgv = pg_v;
         pg_v = pg_k;
         pg_k = page_of(t + 3);
-        const Offs o = offs();
         const uint32_t kbase = PAR * kPipeKTile + o.kr;
         const uint32_t kdst = (PAR ^ 1) * kPipeKTile + o.k_loff;
         const uint32_t vdst = kPipeV0 + PAR * kPipeVTile + o.v_loff;
@@ -2031,11 +2031,26 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
             kf[st][1] = *(const lds_f16x8 *)lds_at(kbase + 32 * kPipeKPitch + st * 32);
         };
         f32x16 sacc[2];
+        // V^T fragments of the P V product, read kVAhead MFMAs ahead of
+        // their use; the first ones during the S product's last k-steps
+        constexpr int kVAhead = 4;
+        const uint32_t vbase = kPipeV0 + (PAR ^ 1) * kPipeVTile + o.vr;
+        auto vfrag = [&](int i) __attribute__((always_inline)) {
+            const int st = i >> 2, tt = i & 3;
+            return *(const lds_f16x8 *)lds_at(vbase + tt * 32 * kPipeVPitch + st * 32);
+        };
+        f16x8 va[16];
+        // K fragments read two k-steps (four MFMAs) ahead of their use
         read_k(0);
+        read_k(1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            if (st + 1 < NS) read_k(st + 1);
+            if (st + 2 < NS) read_k(st + 2);
+            if (HAS_PV && st == NS - 2) {
+#pragma unroll
+                for (int i = 0; i < kVAhead; ++i) va[i] = vfrag(i);
+            }
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st][kb], qop[st],
@@ -2056,20 +2071,12 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
             ls[st] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, ls[st], false);
         };
         if constexpr (HAS_PV) {
-            const uint32_t vbase = kPipeV0 + (PAR ^ 1) * kPipeVTile + o.vr;
-            auto vfrag = [&](int i) __attribute__((always_inline)) {
-                const int st = i >> 2, tt = i & 3;
-                return *(const lds_f16x8 *)lds_at(vbase + tt * 32 * kPipeVPitch + st * 32);
-            };
-            f16x8 va = vfrag(0);
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int st = i >> 2, tt = i & 3;
-                const f16x8 a = va;
-                if (i + 1 < 16) va = vfrag(i + 1);
+                if (i + kVAhead < 16) va[i + kVAhead] = vfrag(i + kVAhead);
                 oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                    a, __builtin_bit_cast(f16x8, pprev[st]), oacc[tt], 0, 0, 0);
+                    va[i], __builtin_bit_cast(f16x8, pprev[st]), oacc[tt], 0, 0, 0);
                 prob_job(i);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -2082,7 +2089,7 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
         __syncthreads();
     };
     auto pv_last = [&](uint32_t vbuf, const u32x4 (&pop)[4]) __attribute__((always_inline)) {
-        const uint32_t vbase = vbuf + offs().vr;
+        const uint32_t vbase = vbuf + o.vr;
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
 #pragma unroll
