@@ -491,7 +491,9 @@ def bench_prefill(args, torch, pkg, steps, warmup):
             "unit": "TFLOP/s",
             "frac": round(call_tflops / MFMA_BF16_PEAK_TFS, 4),
             "traffic": traffic_from_profiles("attn_prefill_qwen3_8b"),
-            "kernel": f"{attn_name}<128,4,true>",
+            # (the pipelined kernel is templated on the group size only)
+            "kernel": (f"{attn_name}<4>" if attn_name == "attn_prefill_pipe_kernel"
+                       else f"{attn_name}<128,4,true>"),
             "launch_us_mean": round(float(attn_us), 2),
             "flops_per_launch": int(step_flops // nchunk),
             "flops_per_step": int(step_flops),
