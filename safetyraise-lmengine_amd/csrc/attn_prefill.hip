@@ -2001,11 +2001,17 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
         // a register set is refilled right after its last conversion
         u32x4 kw;
         uint32_t vlo = 0;
-        auto stage_job = [&](int j) __attribute__((always_inline)) {
+        // Each job in two halves, so that no instruction waits on the one
+        // before it: stage_unpack(j) widens the job's two bf16 values to f32
+        // (and refills a register set once its last values are out),
+        // stage_pack(j) (one MFMA later) rounds them to an fp16 pair and
+        // stores the chunk or piece the pair completes.
+        float uf[16][2];
+        auto stage_unpack = [&](int j) __attribute__((always_inline)) {
             if (j < 8) {
                 const int i = j >> 2, w = j & 3;
-                kw[w] = pack_f16x2(bf16lo(sk[i][w]), bf16hi(sk[i][w]));
-                if (w == 3) *(lds_u32x4 *)lds_at(kdst + i * kPipeKPitch) = kw;
+                uf[j][0] = bf16lo(sk[i][w]);
+                uf[j][1] = bf16hi(sk[i][w]);
                 if (j == 7) load_k(sk, tile_ptr(p.k_pages, t + 2, pgk), o.k_goff);
             } else {
                 const int jj = j - 8, e = jj >> 1, hi = jj & 1;
@@ -2015,14 +2021,21 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
                         if (4 * vg + q >= valid) sv[q] = u32x2{0, 0};
                 }
                 const uint32_t w0 = sv[2 * hi][e >> 1], w1 = sv[2 * hi + 1][e >> 1];
-                const uint32_t pr = (e & 1) ? pack_f16x2(bf16hi(w0), bf16hi(w1))
-                                            : pack_f16x2(bf16lo(w0), bf16lo(w1));
-                if (!hi) {
-                    vlo = pr;
-                } else {
-                    *(lds_u32x2 *)lds_at(vdst + e * kPipeVPitch) = u32x2{vlo, pr};
-                }
+                uf[j][0] = (e & 1) ? bf16hi(w0) : bf16lo(w0);
+                uf[j][1] = (e & 1) ? bf16hi(w1) : bf16lo(w1);
                 if (j == 15) load_v(sv, tile_ptr(p.v_pages, t + 1, pgv), o.v_goff);
+            }
+        };
+        auto stage_pack = [&](int j) __attribute__((always_inline)) {
+            const uint32_t pr = pack_f16x2(uf[j][0], uf[j][1]);
+            if (j < 8) {
+                const int i = j >> 2, w = j & 3;
+                kw[w] = pr;
+                if (w == 3) *(lds_u32x4 *)lds_at(kdst + i * kPipeKPitch) = kw;
+            } else {
+                const int jj = j - 8, e = jj >> 1, hi = jj & 1;
+                if (!hi) vlo = pr;
+                else *(lds_u32x2 *)lds_at(vdst + e * kPipeVPitch) = u32x2{vlo, pr};
             }
         };
         f16x8 kf[NS][2];
@@ -2055,17 +2068,29 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
             for (int kb = 0; kb < 2; ++kb) {
                 sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[st][kb], qop[st],
                                                                   st ? sacc[kb] : negm, 0, 0, 0);
-                stage_job(2 * st + kb);
+                stage_unpack(2 * st + kb);
+                if (st + kb > 0) stage_pack(2 * st + kb - 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        stage_pack(15);
         softmax_mask1<MASKED>(sacc, t * kKeyTile, key_limit, h);
         // probability job j: the pair j & 3 of k-step j / 4
+        // probability pair j (the pair j & 3 of k-step j / 4) in two halves,
+        // so that no instruction waits on the one before it: exp_job(j) takes
+        // the two exps, pack_job(j) (one MFMA later) packs them and adds the
+        // pair to the row sum
         float ls[4] = {};
-        auto prob_job = [&](int j) __attribute__((always_inline)) {
+        float ex[16][2];
+        auto exp_job = [&](int j) __attribute__((always_inline)) {
             const int st = j >> 2, pr = j & 3;
             const int e = 8 * (st & 1) + 2 * pr;
-            const uint32_t w = pack_f16x2(fast_exp2(sacc[st >> 1][e]), fast_exp2(sacc[st >> 1][e + 1]));
+            ex[j][0] = fast_exp2(sacc[st >> 1][e]);
+            ex[j][1] = fast_exp2(sacc[st >> 1][e + 1]);
+        };
+        auto pack_job = [&](int j) __attribute__((always_inline)) {
+            const int st = j >> 2, pr = j & 3;
+            const uint32_t w = pack_f16x2(ex[j][0], ex[j][1]);
             pcur[st][pr] = w;
             const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
             ls[st] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), one, ls[st], false);
@@ -2077,12 +2102,17 @@ attn_prefill_pipe_kernel(const PrefillParams p) {
                 if (i + kVAhead < 16) va[i + kVAhead] = vfrag(i + kVAhead);
                 oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                     va[i], __builtin_bit_cast(f16x8, pprev[st]), oacc[tt], 0, 0, 0);
-                prob_job(i);
+                exp_job(i);
+                if (i > 0) pack_job(i - 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            pack_job(15);
         } else {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) prob_job(j);
+            for (int j = 0; j < 16; ++j) {
+                exp_job(j);
+                pack_job(j);
+            }
         }
         const float lt = (ls[0] + ls[1]) + (ls[2] + ls[3]);
         softmax_fixup1<D>(sacc, t == 0, lt, m_run, negm, l_run, oacc, pcur);
