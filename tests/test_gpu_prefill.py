@@ -104,6 +104,38 @@ def test_qwen35_gated_partial_rope_prefill(pkg, backend, rng):
     pool.destroy()
 
 
+@pytest.mark.parametrize("heads,kv_heads,gated,qk_norm", [(16, 4, True, True),
+                                                          (16, 8, True, True),
+                                                          (32, 4, False, False)])
+def test_head_dim_128_gate_mrope_offset_and_no_norm(pkg, backend, rng, heads, kv_heads,
+                                                    gated, qk_norm):
+    # head_dim 128 at page 64 (the pipelined kernel's shapes, G = 4, 2, 8):
+    # the per-head q/gate interleave with the sigmoid gate on the output,
+    # MRoPE sections over a partial rotary span with the norm offset, and a
+    # layer without QK-norm
+    pool = new_pool(pkg, backend, kv_heads, 128, max_tokens=1024, seqs=2)
+    if qk_norm:
+        gq = (0.02 * rng.standard_normal(128)).astype(np.float32)
+        gk = (0.02 * rng.standard_normal(128)).astype(np.float32)
+        extra = dict(rotary=96, theta=1e7, gq=gq, gk=gk, offset=True, mrope=(16, 16, 16))
+        axes = (0, 3, 7)
+    else:
+        extra = dict(rotary=128)
+        axes = None
+    cases = [Case(rng, pool, heads, kv_heads, 128, ctx=100, rows=70, gated=gated,
+                  qk_norm=qk_norm, pos_axes=axes),
+             Case(rng, pool, heads, kv_heads, 128, ctx=0, rows=150, gated=gated,
+                  qk_norm=qk_norm, pos_axes=axes)]
+    backend.timing(True)
+    try:
+        run_case(pkg, backend, pool, cases, gated=gated, **extra)
+        ran = backend.kernel_times()
+    finally:
+        backend.timing(False)
+    assert "attn_prefill_pipe_kernel" in ran, sorted(ran)
+    pool.destroy()
+
+
 def test_mixed_batch_prefill_decode_and_verify_rows(pkg, backend, rng):
     # one call: a prefill chunk, a decode row and a 5-row verify block
     pool = new_pool(pkg, backend, 8, 128, max_tokens=2048, seqs=3)
