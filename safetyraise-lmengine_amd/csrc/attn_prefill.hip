@@ -149,10 +149,11 @@ __device__ __forceinline__ float sum_f16x8(const f16x8 &x, float acc) {
 }
 
 // ---------------------------------------------------------------------------
-// K/V append of every new row.  16 lanes per (row, KV head), D/16 contiguous
-// elements per lane (one 16-byte load per tensor at D = 128), four heads per
-// wave; the KV heads of a row are consecutive waves.  Work items are
-// independent and short, so the whole call's loads are in flight together.
+// K/V append of every new row.  One wave per row: 16 lanes per KV head, D/16
+// contiguous elements per lane (one 16-byte load per tensor at D = 128), four
+// heads per pass and two passes' loads in flight together; the row's RoPE
+// table is computed once.  Rows are independent and short, so the whole
+// call's loads are in flight together.
 // ---------------------------------------------------------------------------
 constexpr int kAppendHeadsPerWave = 4;
 
@@ -215,11 +216,12 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     constexpr int HW = kAppendHeadsPerWave;
     __shared__ float cs_s[4][D / 2];
     __shared__ float sn_s[4][D / 2];
-    __shared__ __align__(16) float xs[4][HW][D];  // normalised K, for the rotate-half partners
+    // normalised K of two head quads, for the rotate-half partners
+    __shared__ __align__(16) float xs[4][2][HW][D];
     const int tid = threadIdx.x;
     const int wave = wave_index();
     const int lane = tid & 63;
-    const int slot = lane >> 4;  // head of the wave this lane works on
+    const int slot = lane >> 4;  // head of the quad this lane works on
     const int l16 = lane & 15;
     const PrefillMeta m = p.meta[blockIdx.y];
     // the kernel arguments used below, read in one batch and waited for once
@@ -229,11 +231,15 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
              bpt = (uint64_t)p.page_table, bpos = (uint64_t)p.positions, bcs = (uint64_t)p.rope_cs,
              berr = (uint64_t)p.err_word, bkp = (uint64_t)p.k_pages, bvp = (uint64_t)p.v_pages;
     uint32_t kv_heads = p.cache_kv_heads, flags = p.flags, pages_per_seq = p.pages_per_seq,
-             lpt = p.log2_page_tokens, rotary_dim = p.rotary_dim, num_pages = p.num_pages;
+             lpt = p.log2_page_tokens, rotary_dim = p.rotary_dim, num_pages = p.num_pages,
+             tbl_n = p.tbl_n, m_slot = m.slot, m_ctx = m.ctx, m_rows = m.rows, m_row0 = m.row0;
+    uint32_t mrope[3] = {p.mrope[0], p.mrope[1], p.mrope[2]};
     float eps = p.eps;
     asm volatile("" : "+s"(bk), "+s"(bv), "+s"(bkn), "+s"(bpt), "+s"(bpos), "+s"(bcs), "+s"(berr),
                  "+s"(bkp), "+s"(bvp), "+s"(kv_heads), "+s"(flags), "+s"(pages_per_seq), "+s"(lpt),
-                 "+s"(rotary_dim), "+s"(num_pages), "+s"(eps));
+                 "+s"(rotary_dim), "+s"(num_pages), "+s"(eps), "+s"(tbl_n), "+s"(m_slot),
+                 "+s"(m_ctx), "+s"(m_rows), "+s"(m_row0), "+s"(mrope[0]), "+s"(mrope[1]),
+                 "+s"(mrope[2]));
     const void *k_in = global_from_bits<const void>(bk);
     const void *v_in = global_from_bits<const void>(bv);
     const float *k_norm = global_from_bits<const float>(bkn);
@@ -247,40 +253,29 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     // the kernels that follow; every row takes its own page from the list
     // (the table itself may not hold it yet)
     if (blockIdx.x == 0 && blockIdx.y == 0) {
-        for (uint32_t i = tid; i < p.tbl_n; i += 256) {
-            ((int32_t *)p.page_table)[p.tbl_idx[i]] = p.tbl_val[i];
+        for (uint32_t i = tid; i < tbl_n; i += 256) {
+            ((int32_t *)page_table)[p.tbl_idx[i]] = p.tbl_val[i];
         }
     }
-    // no barrier below, so a wave past the rows just ends
-    const uint32_t quads = (kv_heads + HW - 1) / HW;
-    const uint32_t w = blockIdx.x * 4 + wave;
-    const uint32_t r = w / quads;
-    const uint32_t quad = w - r * quads;
-    if (r >= m.rows) return;
-    const uint32_t row = m.row0 + r;
+    // one wave per row (all its KV heads); no barrier below, so a wave past
+    // the rows just ends
+    const uint32_t r = blockIdx.x * 4 + wave;
+    if (r >= m_rows) return;
+    const uint32_t row = m_row0 + r;
     // the input type is a template parameter: a run-time branch around the
     // span loads would end each in a wait for every load in flight
     constexpr bool bf16_in = kBf16In;
     const bool qk_norm = (flags & SAFETYRAISE_MI355X_QK_NORM) != 0;
     const bool interleaved = (flags & SAFETYRAISE_MI355X_MROPE_INTERLEAVED) != 0;
     const float norm_add = (flags & SAFETYRAISE_MI355X_NORM_OFFSET) ? 1.0f : 0.0f;
+    const uint32_t quads = (kv_heads + HW - 1) / HW;
+    const uint32_t e0 = l16 * EPL;  // first element of this lane
 
-    const uint32_t kvh_raw = quad * HW + slot;
-    const bool head_ok = kvh_raw < kv_heads;
-    const uint32_t kvh = min(kvh_raw, kv_heads - 1);  // lanes past the heads repeat the last
-    const uint32_t e0 = l16 * EPL;                     // first element of this lane
-    const size_t src = ((size_t)row * kv_heads + kvh) * D + e0;
-    float x[EPL], vv[EPL], wk[EPL];
-    load_span<EPL>(k_in, src, bf16_in, x);
-    load_span<EPL>(v_in, src, bf16_in, vv);
-    load_span<EPL>(k_norm, e0, false, wk);  // readable without QK-norm too
-
-    const uint32_t tok = m.ctx + r;
-    const uint32_t tidx = m.slot * pages_per_seq + (tok >> lpt);
-    int32_t page = page_table[tidx];
     // the RoPE table's inputs (the row's three position axes, this lane's
-    // frequency denominators) are requested before the first wait below, so
-    // the wave waits for one memory round trip
+    // frequency denominators) and the row's page are requested first, then
+    // the K/V of two head quads at a time (the second repeats the last head
+    // when the row has fewer), with no wait in between: the table is computed
+    // while the K/V loads are in flight
     const uint32_t half = rotary_dim / 2;
     constexpr int NTAB = (D / 2 + 63) / 64;  // table entries per lane
     const int32_t *pos3 = positions + (size_t)row * 3;
@@ -288,85 +283,132 @@ __global__ __launch_bounds__(256) void kv_append_rows_kernel(const PrefillParams
     float den[NTAB];
 #pragma unroll
     for (int k = 0; k < NTAB; ++k) den[k] = p.rope.denom[min((uint32_t)lane + 64 * k, half - 1)];
+    const uint32_t tok = m_ctx + r;
+    const uint32_t tidx = m_slot * pages_per_seq + (tok >> lpt);
+    int32_t page = page_table[tidx];
+    const uint32_t ti = p.tbl_idx[min((uint32_t)lane, kInlineTable - 1)];
+    float x[2][EPL], vv[2][EPL];
+    uint32_t kvh[2];
+    bool head_ok[2];
+    auto load_quads = [&](uint32_t q0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t kvh_raw = (q0 + j) * HW + slot;
+            head_ok[j] = kvh_raw < kv_heads;
+            kvh[j] = min(kvh_raw, kv_heads - 1);
+            const size_t src = ((size_t)row * kv_heads + kvh[j]) * D + e0;
+            load_span<EPL>(k_in, src, bf16_in, x[j]);
+            load_span<EPL>(v_in, src, bf16_in, vv[j]);
+        }
+    };
+    load_quads(0);
+    float wk[EPL];
+    load_span<EPL>(k_norm, e0, false, wk);  // readable without QK-norm too
     {
-        const bool hit = (uint32_t)lane < p.tbl_n && p.tbl_idx[min((uint32_t)lane, kInlineTable - 1)] == tidx;
-        const uint64_t mask = __builtin_amdgcn_ballot_w64(hit);
+        const uint64_t mask = __builtin_amdgcn_ballot_w64((uint32_t)lane < tbl_n && ti == tidx);
         if (mask != 0) page = p.tbl_val[__builtin_ctzll(mask)];
     }
     const uint32_t pt_mask = (1u << lpt) - 1;
+    const size_t dst_tok = (((size_t)page << lpt) + (tok & pt_mask)) * D + e0;
+    const size_t head_stride = ((size_t)num_pages << lpt) * D;
 
     // RoPE angle of pair i: pos[axis(i)] / theta^(2i/rotary_dim) with an IEEE
-    // f32 division (math.rs:90-91); each wave of the row computes the row's
-    // table, the first also saves it for the q side
+    // f32 division (math.rs:90-91); the row's table, saved for the q side at
+    // the end (a store issued here would hold up the wait for the K/V loads)
+    float tab_cs[NTAB], tab_sn[NTAB];
 #pragma unroll
     for (int k = 0; k < NTAB; ++k) {
         const uint32_t i = lane + 64 * k;
         if (i < half) {
-            const int axis = rope_axis(i, p.mrope, interleaved);
+            const int axis = rope_axis(i, mrope, interleaved);
             const int32_t pos = axis == 0 ? pz0 : axis == 1 ? pz1 : pz2;
             const float angle = (float)pos / den[k];
-            float sn, cs;
-            sincosf(angle, &sn, &cs);
-            cs_s[wave][i] = cs;
-            sn_s[wave][i] = sn;
-            if (quad == 0) rope_cs[(size_t)row * half + i] = make_float2(cs, sn);
-        }
-    }
-    if (qk_norm) {
-        // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) ss += x[i] * x[i];
-        ss = sum16(ss);
-        const float variance = ss / (float)D;
-        if (!isfinite(variance) && l16 == 0 && head_ok) atomicOr(err_word, kErrNonFiniteVariance);
-        const float inv = 1.0f / sqrtf(variance + eps);
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) x[i] = x[i] * inv * (wk[i] + norm_add);
-    }
-    // rotate-half over the first rotary_dim dims (math.rs:52-99): element e
-    // pairs with e +- half, held by another lane of the same head; the
-    // partners go through this wave's LDS (LDS operations of one wave are
-    // performed in order, so no barrier is needed)
-#pragma unroll
-    for (int c = 0; c < EPL / 4; ++c) {
-        *(float4 *)&xs[wave][slot][e0 + 4 * c] = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float y[EPL];
-#pragma unroll
-    for (int i = 0; i < EPL; ++i) {
-        const uint32_t e = e0 + i;
-        y[i] = x[i];
-        if (e < rotary_dim) {
-            const bool lo = e < half;
-            const uint32_t pi = lo ? e : e - half;
-            const float partner = xs[wave][slot][lo ? e + half : e - half];
-            const float cs = cs_s[wave][pi], sn = sn_s[wave][pi];
-            y[i] = lo ? x[i] * cs - partner * sn : x[i] * cs + partner * sn;
+            sincosf(angle, &tab_sn[k], &tab_cs[k]);
+            cs_s[wave][i] = tab_cs[k];
+            sn_s[wave][i] = tab_sn[k];
         }
     }
     bool finite = true;
+    for (uint32_t q0 = 0;;) {
+        if (qk_norm) {
+            // rms_norm (math.rs:28-50): x * (1/sqrt(mean(x^2)+eps)) * (w + offset)
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) finite = finite && isfinite(y[i]) && isfinite(vv[i]);
-    if (head_ok) {
-        const size_t dst = ((((size_t)kvh * num_pages + page) << lpt) + (tok & pt_mask)) * D + e0;
-        store_span_bf16<EPL>(k_pages, dst, y);
-        store_span_bf16<EPL>(v_pages, dst, vv);
+            for (int j = 0; j < 2; ++j) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) ss += x[j][i] * x[j][i];
+                ss = sum16(ss);
+                const float variance = ss / (float)D;
+                if (!isfinite(variance) && l16 == 0 && head_ok[j]) {
+                    atomicOr(err_word, kErrNonFiniteVariance);
+                }
+                const float inv = 1.0f / sqrtf(variance + eps);
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) x[j][i] = x[j][i] * inv * (wk[i] + norm_add);
+            }
+        }
+        // rotate-half over the first rotary_dim dims (math.rs:52-99): element
+        // e pairs with e +- half, held by another lane of the same head; the
+        // partners go through this wave's LDS (LDS operations of one wave are
+        // performed in order, so no barrier is needed).  Every read is issued
+        // (indices clamped into the arrays) before the one wait, and the
+        // unrotated dims keep x.
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int c = 0; c < EPL / 4; ++c) {
+                *(float4 *)&xs[wave][j][slot][e0 + 4 * c] =
+                    make_float4(x[j][4 * c], x[j][4 * c + 1], x[j][4 * c + 2], x[j][4 * c + 3]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float y[2][EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const uint32_t e = e0 + i;
+            const bool lo = e < half;
+            const uint32_t pi = min(lo ? e : e - half, (uint32_t)(D / 2 - 1));
+            const uint32_t pe = min(lo ? e + half : e - half, (uint32_t)(D - 1));
+            const float cs = cs_s[wave][pi], sn = sn_s[wave][pi];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float partner = xs[wave][j][slot][pe];
+                const float rot = lo ? x[j][i] * cs - partner * sn : x[j][i] * cs + partner * sn;
+                y[j][i] = e < rotary_dim ? rot : x[j][i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) ok = ok && isfinite(y[j][i]) && isfinite(vv[j][i]);
+            finite = finite && (ok || !head_ok[j]);
+            if (head_ok[j]) {
+                const size_t dst = kvh[j] * head_stride + dst_tok;
+                store_span_bf16<EPL>(k_pages, dst, y[j]);
+                store_span_bf16<EPL>(v_pages, dst, vv[j]);
+            }
+        }
+        q0 += 2;
+        if (q0 >= quads) break;
+        load_quads(q0);
     }
-    if (__builtin_amdgcn_ballot_w64(head_ok && !finite) != 0 && lane == 0) {
+#pragma unroll
+    for (int k = 0; k < NTAB; ++k) {
+        const uint32_t i = lane + 64 * k;
+        if (i < half) rope_cs[(size_t)row * half + i] = make_float2(tab_cs[k], tab_sn[k]);
+    }
+    if (__builtin_amdgcn_ballot_w64(!finite) != 0 && lane == 0) {
         atomicOr(err_word, kErrNonFiniteKv);
     }
 }
 
-// One call's append: (rows x head quads) waves, four per workgroup.
+// One call's append: one wave per row, four per workgroup.
 template <int D>
 void launch_append(hipStream_t stream, const PrefillParams &p, uint32_t max_rows) {
-    const uint32_t quads = (p.cache_kv_heads + kAppendHeadsPerWave - 1) / kAppendHeadsPerWave;
-    const uint32_t waves = max_rows * quads;
-    const dim3 grid((waves + 3) / 4, p.nseq);
+    const dim3 grid((max_rows + 3) / 4, p.nseq);
     if (p.flags & SAFETYRAISE_MI355X_INPUT_BF16) {
         SR_LAUNCH("kv_append_rows_kernel", (kv_append_rows_kernel<D, true>), grid, dim3(256), 0, stream, p);
     } else {

@@ -146,6 +146,56 @@ def test_kv_append_read_layout(pkg, backend):
     pool.destroy()
 
 
+def rounding_rows(rng, rows, width, big=True):
+    """f32 rows whose bf16 rounding covers exact ties (even and odd kept
+    halves), one ulp either side of a tie, random low bits, f32 denormals and
+    (big=True) values next to the largest finite bf16."""
+    hi = rng.standard_normal((rows, width)).astype(np.float32).view(np.uint32) & np.uint32(0xFFFF0000)
+    picks = np.array([0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF], np.uint32)
+    low = np.where(rng.random(hi.shape) < 0.5, rng.choice(picks, size=hi.shape),
+                   rng.integers(0, 1 << 16, size=hi.shape, dtype=np.uint32))
+    x = (hi | low.astype(np.uint32)).view(np.float32).copy()
+    special = [1e-40, -3e-39, 1.1754942e-38, 5e-45, -1e-10, 6e4, 0.0, -0.0]
+    if big:
+        special += [3.38e38, -3.3e38]
+    x[0, :len(special)] = np.array(special, np.float32)
+    return x
+
+
+def bits(x):
+    return np.ascontiguousarray(x, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("rows", [1, 40])
+def test_cache_append_rounds_to_nearest_even_bit_exact(pkg, backend, rng, rows):
+    # the cache stores bf16 rounded to nearest even (the oracle's bf16_round);
+    # both K and V of a plain append are the inputs themselves
+    pool = new_pool(pkg, backend, 2, 128, page_tokens=16, max_tokens=64, seqs=1)
+    seq = pool.open()
+    k = rounding_rows(rng, rows, 256)
+    v = rounding_rows(rng, rows, 256)
+    pool.append(seq, k, v)
+    rk, rv = pool.read(seq)
+    assert np.array_equal(bits(rk), bits(O.bf16_round(k)))
+    assert np.array_equal(bits(rv), bits(O.bf16_round(v)))
+    pool.destroy()
+
+
+@pytest.mark.parametrize("rows", [1, 40])
+def test_attention_append_rounds_v_to_nearest_even_bit_exact(pkg, backend, rng, rows):
+    # the V rows an attention call appends (decode for 1 row, the prefill
+    # append kernel for 40) are the inputs rounded to bf16, bit for bit
+    pool = new_pool(pkg, backend, 8, 128, max_tokens=256, seqs=1)
+    gq = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    gk = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+    case = Case(rng, pool, 32, 8, 128, ctx=20, rows=rows)
+    case.v = rounding_rows(rng, rows, 8 * 128, big=False)
+    run_case(pkg, backend, pool, [case], rotary=128, gq=gq, gk=gk)
+    _, rv = pool.read(case.seq, 20, rows)
+    assert np.array_equal(bits(rv), bits(O.bf16_round(case.v)))
+    pool.destroy()
+
+
 def test_kv_truncate_restores_without_losing_prior_rows(pkg, backend):
     # src/gpu.rs:6490-6518
     pool = new_pool(pkg, backend, 1, 64, page_tokens=16, max_tokens=8, seqs=2)
