@@ -619,7 +619,9 @@ __global__ void __launch_bounds__(256) gdn_rollback_kernel(const RollbackParams 
 //     all chunks of the call at once; writes a record per (chunk, value head):
 //       Qe = diag(e^{g_t} / |q_t|) Q,  -W,  U,  Ks = K^T diag(e^{g_C-g_j} / |k_j|),
 //       Pm[t][j] = e^{g_t-g_j} (q^_t . k^_j) (j <= t),  e^{g_C}
-//     and, from the last chunk, the next conv history;
+//     and, from the last chunk, the next conv history (the records with
+//     nontemporal stores: the scan reads them on other XCDs, from memory
+//     anyway, and streaming them out took 0.5 us off the kernel);
 //   gdn_chunk_scan_kernel: one workgroup per (sequence, value head, 32 of the
 //     Dv = 128 state rows), the slice in LDS, walking the chunks in order:
 //       Delta = U + (-W) S0^T,  o = (Qe S0^T + Pm Delta) / sqrt(Dk),
@@ -1065,8 +1067,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
         // Ks[d][j] = k[d][j] e^{g_C - g_j} / |k_j|
         for (int e = first; e < kDk * kCk / 4; e += stride) {
             const int d = e >> 3, j = 4 * (e & 7);
-            *(f32x4 *)(rec + kRecKs + d * kCk + j) =
-                *(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j];
+            __builtin_nontemporal_store(*(const f32x4 *)&L.kc[d][j] * *(const f32x4 *)&L.ss[j],
+                                        (f32x4 *)(rec + kRecKs + d * kCk + j));
         }
     };
     if (wave < 3 || kW) {
@@ -1110,7 +1112,8 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
             // Qe = diag(e^{g_t} / |q_t|) Q
             const int e = u + n * 256;
             const int t = e >> 5, d = 4 * (e & 31);
-            *(f32x4 *)(rec + kRecQe + t * kDk + d) = *(const f32x4 *)&L.qv.q[t][d] * L.qs[t];
+            __builtin_nontemporal_store(*(const f32x4 *)&L.qv.q[t][d] * L.qs[t],
+                                        (f32x4 *)(rec + kRecQe + t * kDk + d));
         }
         if (kU) write_ks(u, 256);
     } else {
@@ -1208,7 +1211,7 @@ __global__ void __launch_bounds__(kPrepThreads) gdn_chunk_prep_kernel(const GdnP
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int t = 16 * tr + 4 * sl + i, col = c0 + 16 * n + r16;
-                    dst[t * kDk + col] = sign * o[n][i];
+                    __builtin_nontemporal_store(sign * o[n][i], dst + t * kDk + col);
                 }
         };
         if (kW) product(L.sw, L.kc, rec + kRecWn, -1.0f);
